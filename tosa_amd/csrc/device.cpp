@@ -1,0 +1,175 @@
+#include "device.h"
+
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+namespace tosa {
+
+void hip_check(hipError_t e, const char* what)
+{
+    if (e != hipSuccess)
+        throw Error(ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+std::string device_error_message(uint32_t bits)
+{
+    std::string m;
+    if (bits & DERR_SCALE_PARAMS)
+        m += "apply_scale: invalid multiplier or shift; ";
+    if (bits & DERR_SCALE_RANGE)
+        m += "apply_scale_32: value out of range for shift; ";
+    if (bits & DERR_SCALE_RESULT)
+        m += "apply_scale: result exceeds int32; ";
+    if (bits & DERR_RESCALE_I32)
+        m += "RESCALE: result exceeds the int32 range; ";
+    if (!m.empty())
+        m.resize(m.size() - 2);
+    return m;
+}
+
+namespace {
+
+struct Pools {
+    std::mutex mu;
+    // stream -> (size -> free blocks)
+    std::unordered_map<hipStream_t, std::multimap<size_t, void*>> free;
+    size_t cached = 0;
+};
+
+Pools& pools()
+{
+    static Pools* p = new Pools();  // never destroyed: blocks may be freed during exit
+    return *p;
+}
+
+size_t round_size(size_t b)
+{
+    if (b <= 256)
+        return 256;
+    if (b <= (1u << 20)) {  // next power of two up to 1 MiB
+        size_t r = 512;
+        while (r < b)
+            r <<= 1;
+        return r;
+    }
+    const size_t g = 2u << 20;  // 2 MiB granules above
+    return (b + g - 1) / g * g;
+}
+
+thread_local Stream* t_stream = nullptr;
+thread_local hipStream_t t_user_stream = nullptr;
+
+std::mutex g_err_mu;
+std::unordered_map<hipStream_t, uint32_t*> g_err_words;
+
+uint32_t* error_word_for(hipStream_t s)
+{
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    auto it = g_err_words.find(s);
+    if (it != g_err_words.end())
+        return it->second;
+    void* p = nullptr;
+    hip_check(hipMalloc(&p, 256), "hipMalloc(error word)");
+    hip_check(hipMemset(p, 0, 256), "hipMemset(error word)");
+    g_err_words[s] = static_cast<uint32_t*>(p);
+    return static_cast<uint32_t*>(p);
+}
+
+}  // namespace
+
+int device_count()
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess)
+        return 0;
+    return n;
+}
+
+bool device_available() { return device_count() > 0; }
+
+Stream& thread_stream()
+{
+    if (t_user_stream) {
+        static thread_local Stream user;
+        if (user.s != t_user_stream) {
+            user.s = t_user_stream;
+            user.err = error_word_for(t_user_stream);
+        }
+        return user;
+    }
+    if (!t_stream) {
+        if (!device_available())
+            throw Error(ERR_DEVICE, "no HIP device is available (the MI355X path needs a GPU)");
+        Stream* st = new Stream();
+        hip_check(hipStreamCreateWithFlags(&st->s, hipStreamNonBlocking), "hipStreamCreate");
+        st->err = error_word_for(st->s);
+        t_stream = st;
+    }
+    return *t_stream;
+}
+
+void set_thread_stream(hipStream_t s) { t_user_stream = s; }
+
+void* dev_alloc(size_t bytes, hipStream_t s)
+{
+    size_t r = round_size(bytes);
+    Pools& P = pools();
+    {
+        std::lock_guard<std::mutex> lk(P.mu);
+        auto& m = P.free[s];
+        auto it = m.find(r);
+        if (it != m.end()) {
+            void* p = it->second;
+            m.erase(it);
+            P.cached -= r;
+            return p;
+        }
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, r);
+    if (e == hipErrorOutOfMemory) {
+        // Return every cached block to the driver and try once more.
+        std::lock_guard<std::mutex> lk(P.mu);
+        (void)hipDeviceSynchronize();
+        for (auto& [st, m] : P.free)
+            for (auto& [sz, q] : m)
+                (void)hipFree(q);
+        P.free.clear();
+        P.cached = 0;
+        e = hipMalloc(&p, r);
+    }
+    hip_check(e, "hipMalloc");
+    return p;
+}
+
+void dev_free(void* p, size_t bytes, hipStream_t s)
+{
+    if (!p)
+        return;
+    size_t r = round_size(bytes);
+    Pools& P = pools();
+    std::lock_guard<std::mutex> lk(P.mu);
+    P.free[s].emplace(r, p);
+    P.cached += r;
+}
+
+size_t dev_cached_bytes()
+{
+    Pools& P = pools();
+    std::lock_guard<std::mutex> lk(P.mu);
+    return P.cached;
+}
+
+void clear_error_word(Stream& st) { hip_check(hipMemsetAsync(st.err, 0, sizeof(uint32_t), st.s), "clear error word"); }
+
+uint32_t read_error_word(Stream& st)
+{
+    uint32_t v = 0;
+    hip_check(hipMemcpyAsync(&v, st.err, sizeof(uint32_t), hipMemcpyDeviceToHost, st.s), "read error word");
+    hip_check(hipStreamSynchronize(st.s), "hipStreamSynchronize");
+    return v;
+}
+
+}  // namespace tosa

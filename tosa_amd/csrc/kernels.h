@@ -1,0 +1,177 @@
+// Host-side launchers of the gfx950 kernels. Every pointer is a device
+// pointer; every launcher enqueues on `stream` and returns immediately.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+namespace tosa {
+namespace kern {
+
+// n / d for 0 <= n < 2^31 with a multiply-high and a shift (d >= 1).
+struct FastDiv {
+    uint32_t d = 1, m = 1, s = 0;
+    FastDiv() = default;
+    explicit FastDiv(uint32_t div);
+};
+
+// RESCALE applied per element (src/ops/type_conv.rs:171-188), optionally
+// followed by a CLAMP (src/ops/elementwise.rs:328-334). Multiplier and shift
+// are validated on the host before launch (multiplier >= 0, shift in
+// [2, 62] unless INEXACT), so kernels only check the value-dependent
+// REQUIRE conditions.
+struct RescaleDev {
+    const int32_t* mult = nullptr;  // [channels]
+    const int32_t* shift = nullptr; // [channels]
+    int32_t channels = 1;           // per-channel: channel = flat index % channels
+    int32_t per_channel = 0;
+    int32_t scale32 = 1;            // 0: 16-bit multiplier (apply_scale_16)
+    int32_t rounding = 1;           // 1 SINGLE, 2 INEXACT, 3 DOUBLE
+    int32_t in_bits = 32;           // input type width, for unsigned extension
+    int32_t in_unsigned = 0;
+    int64_t in_zp = 0, out_zp = 0;  // already extended
+    int64_t lo = 0, hi = 0;         // output range (signed or unsigned)
+    int32_t has_clamp = 0;
+    int64_t clamp_lo = 0, clamp_hi = 0;
+    int32_t out_bytes = 1;          // 1, 2 or 4
+};
+
+// Epilogue of a GEMM-shaped operator.
+enum Epilogue : int32_t {
+    EPI_I32 = 0,      // int32 accumulator + bias, written as int32
+    EPI_RESCALE = 1,  // int32 accumulator + bias, then RescaleDev
+    EPI_FLOAT = 2,    // fp32 accumulator: out = round(round(acc) + bias)
+};
+
+// Float storage formats used by the float epilogues.
+enum FloatFmt : int32_t { FMT_F32 = 0, FMT_F16 = 1, FMT_BF16 = 2, FMT_FP8E4M3 = 3, FMT_FP8E5M2 = 4 };
+
+enum GemmElem : int32_t { ELEM_I8 = 0, ELEM_BF16 = 1, ELEM_F16 = 2 };
+
+// Implicit-GEMM convolution or batched matmul on MFMA.
+//   conv:   x NHWC [n,ih,iw,ic], w OHWI [oc,kh,kw,ic] -> out NHWC [n,oh,ow,oc]
+//   matmul: a [n,h,c], b [n,c,w] -> out [n,h,w]
+struct GemmDesc {
+    int32_t is_conv = 1;
+    GemmElem elem = ELEM_I8;
+    // conv geometry
+    int32_t n = 1, ih = 1, iw = 1, ic = 1, oc = 1, kh = 1, kw = 1, oh = 1, ow = 1;
+    int32_t pt = 0, pl = 0, sy = 1, sx = 1, dy = 1, dx = 1;
+    // matmul geometry
+    int32_t batch = 1, h = 1, c = 1, w = 1;
+    // int8 zero points: x/a side and w/b side
+    int32_t zp_x = 0, zp_w = 0;
+    const int32_t* wsum = nullptr;  // conv: per-oc sum of weights (needed when zp_x != 0)
+    const void* bias = nullptr;     // conv only: int32 (int path) or f32 values (float path)
+    int32_t bias_len = 0;
+    Epilogue epi = EPI_I32;
+    RescaleDev rs;
+    FloatFmt out_fmt = FMT_F32;
+};
+
+void gemm(const GemmDesc& d, const void* x, const void* w, void* out, uint32_t* err, hipStream_t stream);
+
+// Per-output-channel sum of an OHWI int8 weight: wsum[o] = sum_k w[o][k]
+// (mod 2^32).
+void weight_sums_i8(const int8_t* w, int32_t oc, int32_t k, int32_t* wsum, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Reference-order kernels (one thread per output, the reference's loop
+// order and rounding, so float results are bit-identical to a sequential
+// evaluation). They cover every type combination the MFMA path does not.
+// ---------------------------------------------------------------------------
+enum AccKind : int32_t {
+    ACC_I32 = 0, ACC_I64 = 1,                 // integer: wrap mod 2^32 / INT48 clamp
+    ACC_F32 = 2, ACC_F16 = 3, ACC_BF16 = 4,   // accum.rs AccF32 / AccF16 / AccBf16
+    ACC_F16U = 5, ACC_BF16U = 6,              // accum.rs Acc*UnroundedProduct (MATMUL)
+};
+
+// Element codes for the direct kernels' operands.
+enum ElemCode : int32_t {
+    E_I8 = 0, E_I16 = 1, E_I32 = 2, E_I64 = 3,
+    E_F32 = 4, E_F16 = 5, E_BF16 = 6, E_FP8E4M3 = 7, E_FP8E5M2 = 8, E_U8 = 9,
+};
+
+struct DirectConvDesc {
+    int32_t depthwise = 0;
+    int32_t n, ih, iw, c, m, oc, kh, kw, oh, ow, pt, pl, sy, sx, dy, dx;  // c = input channels, m = multiplier
+    ElemCode xe, we, be, oe;  // input, weight, bias and output element codes
+    AccKind acc;
+    int64_t zp_x = 0, zp_w = 0;   // integer zero points
+    float fzp_x = 0, fzp_w = 0;   // float zero points (subtracted as in the reference)
+    int32_t bias_len = 1;
+    int32_t out_fmt = FMT_F32;    // float output rounding format
+};
+void direct_conv(const DirectConvDesc& d, const void* x, const void* w, const void* bias, void* out,
+                 hipStream_t stream);
+
+struct DirectMatmulDesc {
+    int32_t batch, h, c, w;
+    ElemCode ae, be, oe;
+    AccKind acc;
+    int64_t zp_a = 0, zp_b = 0;
+    int32_t out_fmt = FMT_F32;  // operands are rounded to this format first (matmul.rs:160-162)
+};
+void direct_matmul(const DirectMatmulDesc& d, const void* a, const void* b, void* out, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// Bandwidth-bound kernels
+// ---------------------------------------------------------------------------
+
+// int8 DEPTHWISE_CONV2D with depth multiplier 1, int32 accumulation and an
+// I32 / RESCALE epilogue.
+struct DepthwiseDesc {
+    int32_t n, ih, iw, c, kh, kw, oh, ow, pt, pl, sy, sx, dy, dx;
+    int32_t zp_x = 0, zp_w = 0;
+    const int32_t* bias = nullptr;
+    int32_t bias_len = 1;
+    Epilogue epi = EPI_I32;
+    RescaleDev rs;
+};
+// Shapes the int8 depthwise kernel handles: 1x1, 1x3, 3x1, 2x2 and 3x3 taps,
+// channels a multiple of 4. The caller checks this before launching.
+bool depthwise_i8_supported(int kh, int kw, int c);
+void depthwise_i8(const DepthwiseDesc& d, const int8_t* x, const int8_t* w, void* out, uint32_t* err,
+                  hipStream_t stream);
+
+struct PoolDesc {
+    int32_t n, ih, iw, c, kh, kw, oh, ow, pt, pl, sy, sx;
+    ElemCode xe;
+    int64_t in_zp = 0, out_zp = 0, lo = 0, hi = 0;  // integer path
+    int32_t acc_fmt = FMT_F32;                       // float path: accumulator rounding
+    int32_t out_fmt = FMT_F32;                       // float path: output encoding
+};
+void avg_pool2d(const PoolDesc& d, const void* x, void* out, uint32_t* err, hipStream_t stream);
+
+// Standalone RESCALE over `count` elements of element code `xe`.
+void rescale(const RescaleDev& rs, ElemCode xe, const void* x, int64_t count, void* out, uint32_t* err,
+             hipStream_t stream);
+
+// CLAMP: ints compare as int64; floats use nan_max/nan_min
+// (src/ops/common.rs:155-177) and round to the type.
+void clamp(ElemCode e, const void* x, int64_t count, int64_t ilo, int64_t ihi, float flo, float fhi, int nan_ignore,
+           void* out, hipStream_t stream);
+
+// Broadcasting ADD of rank <= 6 operands (src/ops/elementwise.rs:395-397).
+struct BroadcastDesc {
+    int32_t rank = 0;
+    int64_t out_dims[6] = {1, 1, 1, 1, 1, 1};
+    int64_t a_strides[6] = {0}, b_strides[6] = {0};  // element strides, 0 on broadcast dims
+};
+void add(ElemCode e, const BroadcastDesc& bd, const void* a, const void* b, void* out, int64_t count,
+         hipStream_t stream);
+
+// Residual block of a quantised graph, fused: out = RESCALE_o(RESCALE_a(a) +
+// RESCALE_b(b)) where RESCALE_a/b take int8 to int32 and RESCALE_o takes
+// int32 to int8 (equal shapes, no broadcast).
+void residual_add_i8(const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro, const int8_t* a,
+                     const int8_t* b, int64_t count, int64_t channels, void* out, uint32_t* err,
+                     hipStream_t stream);
+
+// TRANSPOSE of a rank <= 6 tensor with elements of `esize` bytes.
+void transpose(const void* x, void* out, int32_t esize, int32_t rank, const int64_t* out_dims,
+               const int64_t* in_strides_permuted, int64_t count, hipStream_t stream);
+
+}  // namespace kern
+}  // namespace tosa

@@ -1,0 +1,504 @@
+// Bandwidth-bound kernels: int8 DEPTHWISE_CONV2D, AVG_POOL2D, RESCALE,
+// CLAMP, ADD, the fused quantised residual add, and TRANSPOSE.
+#include "kcommon.h"
+
+#pragma clang fp contract(off)
+
+namespace tosa {
+namespace kern {
+namespace {
+
+// Bytes j of four words gathered into one word: [x0.bj, x1.bj, x2.bj, x3.bj].
+__device__ __forceinline__ uint32_t gather_byte(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, int j)
+{
+    const int s = 8 * j;
+    return ((x0 >> s) & 0xFFu) | (((x1 >> s) & 0xFFu) << 8) | (((x2 >> s) & 0xFFu) << 16) | (((x3 >> s) & 0xFFu) << 24);
+}
+
+// ---------------------------------------------------------------------------
+// int8 DEPTHWISE_CONV2D, depth multiplier 1, KH*KW <= 12 taps.
+//
+// Replaces Depthwise::accumulate (src/ops/conv.rs:234-266) for int8. A thread
+// owns 4 consecutive channels of PX consecutive output pixels in a row. Taps
+// are grouped four at a time and transposed so that one v_dot4_i32_i8 sums
+// four taps of one channel; zero points are folded exactly as in the
+// implicit GEMM: sum (x~ - zx)(w - zw) = sum x~ w - zw sum x~ - zx sum w +
+// T zx zw, with padding taps loaded as zx.
+// ---------------------------------------------------------------------------
+template <int KH, int KW, int PX>
+__global__ void __launch_bounds__(256) dw_i8_kernel(DepthwiseDesc d, const int8_t* x, const int8_t* w, uint8_t* out,
+                                                    uint32_t* err, int64_t total)
+{
+    constexpr int T = KH * KW;
+    constexpr int G = (T + 3) / 4;
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int cg = d.c >> 2;
+    const int g = int(idx % cg);
+    int64_t r = idx / cg;
+    const int owg = (d.ow + PX - 1) / PX;
+    const int oxq = int(r % owg);
+    r /= owg;
+    const int oy = int(r % d.oh);
+    const int b = int(r / d.oh);
+    const int c0 = 4 * g;
+
+    // Weights [KH][KW][C][1]: words of 4 channels per tap, transposed to 4
+    // taps per channel.
+    uint32_t wt[G][4];
+    int32_t wsum[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < G; q++) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = 4 * q + u;
+            wd[u] = t < T ? *reinterpret_cast<const uint32_t*>(w + int64_t(t) * d.c + c0) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            wt[q][j] = gather_byte(wd[0], wd[1], wd[2], wd[3], j);
+            wsum[j] = __builtin_amdgcn_sdot4(int(wt[q][j]), 0x01010101, wsum[j], false);
+        }
+    }
+    const uint32_t zfill = uint32_t(uint8_t(d.zp_x)) * 0x01010101u;
+    const uint32_t tzz = uint32_t(T) * uint32_t(d.zp_x) * uint32_t(d.zp_w);
+    int32_t bias[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        bias[j] = d.bias ? d.bias[d.bias_len == 1 ? 0 : c0 + j] : 0;
+    uint32_t e = 0;
+
+#pragma unroll
+    for (int px = 0; px < PX; px++) {
+        const int ox = oxq * PX + px;
+        if (ox >= d.ow)
+            break;
+        const int iy0 = oy * d.sy - d.pt, ix0 = ox * d.sx - d.pl;
+        uint32_t acc[4] = {0, 0, 0, 0};
+        int32_t xs[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < G; q++) {
+            uint32_t xd[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int t = 4 * q + u;
+                if (t < T) {
+                    const int iy = iy0 + (t / KW) * d.dy, ix = ix0 + (t % KW) * d.dx;
+                    xd[u] = (unsigned(iy) < unsigned(d.ih) && unsigned(ix) < unsigned(d.iw))
+                                ? *reinterpret_cast<const uint32_t*>(
+                                      x + ((int64_t(b) * d.ih + iy) * d.iw + ix) * d.c + c0)
+                                : zfill;
+                } else {
+                    xd[u] = 0u;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t xt = gather_byte(xd[0], xd[1], xd[2], xd[3], j);
+                acc[j] = uint32_t(__builtin_amdgcn_sdot4(int(xt), int(wt[q][j]), int(acc[j]), false));
+                if (d.zp_w != 0)
+                    xs[j] = __builtin_amdgcn_sdot4(int(xt), 0x01010101, xs[j], false);
+            }
+        }
+        const int64_t o = ((int64_t(b) * d.oh + oy) * d.ow + ox) * d.c + c0;
+        uint32_t v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t a = acc[j] - uint32_t(d.zp_w) * uint32_t(xs[j]) - uint32_t(d.zp_x) * uint32_t(wsum[j]) + tzz +
+                         uint32_t(bias[j]);
+            if (d.epi == EPI_RESCALE) {
+                const int ch = d.rs.per_channel ? c0 + j : 0;
+                a = uint32_t(rescale_value(int64_t(int32_t(a)), d.rs.mult[ch], d.rs.shift[ch], d.rs, e));
+            }
+            v[j] = a;
+        }
+        if (d.epi == EPI_I32) {
+            *reinterpret_cast<uint4*>(out + 4 * o) = uint4{v[0], v[1], v[2], v[3]};
+        } else if (d.rs.out_bytes == 1) {
+            *reinterpret_cast<uint32_t*>(out + o) =
+                (v[0] & 0xFF) | ((v[1] & 0xFF) << 8) | ((v[2] & 0xFF) << 16) | ((v[3] & 0xFF) << 24);
+        } else if (d.rs.out_bytes == 2) {
+            *reinterpret_cast<uint2*>(out + 2 * o) = uint2{(v[0] & 0xFFFF) | (v[1] << 16), (v[2] & 0xFFFF) | (v[3] << 16)};
+        } else {
+            *reinterpret_cast<uint4*>(out + 4 * o) = uint4{v[0], v[1], v[2], v[3]};
+        }
+    }
+    report(err, e);
+}
+
+// ---------------------------------------------------------------------------
+// AVG_POOL2D, src/ops/pool.rs:164-231: padding is excluded from the sum and
+// the divisor; integers divide by reciprocal_scale + apply_scale_32
+// (src/ops/quant.rs:6-32), floats round every add and the divide.
+// ---------------------------------------------------------------------------
+__global__ void avg_pool_kernel(PoolDesc d, const void* x, void* out, uint32_t* err, int64_t total)
+{
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int c = int(idx % d.c);
+    int64_t r = idx / d.c;
+    const int ox = int(r % d.ow);
+    r /= d.ow;
+    const int oy = int(r % d.oh);
+    const int b = int(r / d.oh);
+    const bool is_int = d.xe == E_I8 || d.xe == E_I16;
+    uint32_t acc = 0;
+    float facc = 0.0f;
+    int32_t count = 0;
+    for (int ky = 0; ky < d.kh; ky++) {
+        const int y = oy * d.sy - d.pt + ky;
+        if (y < 0 || y >= d.ih)
+            continue;
+        for (int kx = 0; kx < d.kw; kx++) {
+            const int xx = ox * d.sx - d.pl + kx;
+            if (xx < 0 || xx >= d.iw)
+                continue;
+            const int64_t i = ((int64_t(b) * d.ih + y) * d.iw + xx) * d.c + c;
+            if (is_int)
+                acc += uint32_t(int32_t(load_int(x, i, d.xe) - d.in_zp));
+            else
+                facc = round_fmt(facc + load_float(x, i, d.xe), d.acc_fmt);
+            count++;
+        }
+    }
+    if (is_int) {
+        // reciprocal_scale(count)
+        const uint32_t c1 = uint32_t(count) - 1u;
+        const int k = c1 == 0 ? 0 : 32 - __clz(int(c1));
+        const int64_t numer = ((int64_t(1) << 30) + 1) << k;
+        const int32_t mult = int32_t(numer / count);
+        uint32_t e = 0;
+        const int32_t v = apply_scale_32(int32_t(acc), mult, 30 + k, false, e);
+        report(err, e);
+        int64_t o = int64_t(v) + d.out_zp;
+        o = o < d.lo ? d.lo : (o > d.hi ? d.hi : o);
+        store_int(out, idx, d.xe, o);
+    } else {
+        const float avg = round_fmt(facc / float(count), d.acc_fmt);
+        store_float(out, idx, d.out_fmt, round_fmt(avg, d.out_fmt));
+    }
+}
+
+// Global average pool over 7x7-style windows of int8 (the head of a
+// quantised CNN): 4 channels per thread with word loads.
+__global__ void avg_pool_i8_c4_kernel(PoolDesc d, const int8_t* x, int8_t* out, uint32_t* err, int64_t total)
+{
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int cg = d.c >> 2;
+    const int c0 = 4 * int(idx % cg);
+    int64_t r = idx / cg;
+    const int ox = int(r % d.ow);
+    r /= d.ow;
+    const int oy = int(r % d.oh);
+    const int b = int(r / d.oh);
+    uint32_t acc[4] = {0, 0, 0, 0};
+    int32_t count = 0;
+    for (int ky = 0; ky < d.kh; ky++) {
+        const int y = oy * d.sy - d.pt + ky;
+        if (y < 0 || y >= d.ih)
+            continue;
+        for (int kx = 0; kx < d.kw; kx++) {
+            const int xx = ox * d.sx - d.pl + kx;
+            if (xx < 0 || xx >= d.iw)
+                continue;
+            const uint32_t wv = *reinterpret_cast<const uint32_t*>(x + ((int64_t(b) * d.ih + y) * d.iw + xx) * d.c + c0);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[j] += uint32_t(int32_t(int8_t(wv >> (8 * j))) - int32_t(d.in_zp));
+            count++;
+        }
+    }
+    const uint32_t c1 = uint32_t(count) - 1u;
+    const int k = c1 == 0 ? 0 : 32 - __clz(int(c1));
+    const int64_t numer = ((int64_t(1) << 30) + 1) << k;
+    const int32_t mult = int32_t(numer / count);
+    uint32_t e = 0, packed = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int32_t v = apply_scale_32(int32_t(acc[j]), mult, 30 + k, false, e);
+        int64_t o = int64_t(v) + d.out_zp;
+        o = o < d.lo ? d.lo : (o > d.hi ? d.hi : o);
+        packed |= (uint32_t(o) & 0xFFu) << (8 * j);
+    }
+    report(err, e);
+    *reinterpret_cast<uint32_t*>(out + ((int64_t(b) * d.oh + oy) * d.ow + ox) * d.c + c0) = packed;
+}
+
+// ---------------------------------------------------------------------------
+// RESCALE, src/ops/type_conv.rs:111-191 (per element :174-188).
+// ---------------------------------------------------------------------------
+__global__ void rescale_kernel(RescaleDev rs, int xe, const void* x, int64_t count, void* out, uint32_t* err)
+{
+    uint32_t e = 0;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+        const int ch = rs.per_channel ? int(i % rs.channels) : 0;
+        const int64_t v = rescale_value(load_int(x, i, xe), rs.mult[ch], rs.shift[ch], rs, e);
+        switch (rs.out_bytes) {
+        case 1: static_cast<int8_t*>(out)[i] = int8_t(v); break;
+        case 2: static_cast<int16_t*>(out)[i] = int16_t(v); break;
+        default: static_cast<int32_t*>(out)[i] = int32_t(v); break;
+        }
+    }
+    report(err, e);
+}
+
+// int8 -> int8 RESCALE, 4 elements per thread (channels a multiple of 4).
+__global__ void rescale_i8_c4_kernel(RescaleDev rs, const int8_t* x, int64_t count4, int8_t* out, uint32_t* err)
+{
+    uint32_t e = 0;
+    for (int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; q < count4; q += int64_t(gridDim.x) * blockDim.x) {
+        const uint32_t wv = reinterpret_cast<const uint32_t*>(x)[q];
+        const int ch0 = rs.per_channel ? int((4 * q) % rs.channels) : 0;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int ch = rs.per_channel ? ch0 + j : 0;
+            const int64_t v = rescale_value(int8_t(wv >> (8 * j)), rs.mult[ch], rs.shift[ch], rs, e);
+            packed |= (uint32_t(v) & 0xFFu) << (8 * j);
+        }
+        reinterpret_cast<uint32_t*>(out)[q] = packed;
+    }
+    report(err, e);
+}
+
+// ---------------------------------------------------------------------------
+// CLAMP, src/ops/elementwise.rs:319-343. Floats: nan_max then nan_min
+// (src/ops/common.rs:155-177), rounded to the type.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float nan_pick(float a, float b, int ignore)
+{
+    if (ignore)
+        return (a != a) ? b : a;
+    return __builtin_nanf("");
+}
+
+__global__ void clamp_kernel(int e, const void* x, int64_t count, int64_t ilo, int64_t ihi, float flo, float fhi,
+                             int ignore, void* out)
+{
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+        if (e == E_I8 || e == E_I16) {
+            int64_t v = load_int(x, i, e);
+            v = v > ilo ? v : ilo;
+            v = v < ihi ? v : ihi;
+            store_int(out, i, e, v);
+        } else {
+            const float v = load_float(x, i, e);
+            float m;
+            if (v != v)
+                m = nan_pick(v, flo, ignore);
+            else
+                m = v >= flo ? v : flo;
+            float r;
+            if (m != m)
+                r = nan_pick(m, fhi, ignore);
+            else
+                r = m < fhi ? m : fhi;
+            const int fmt = e == E_F16 ? FMT_F16 : (e == E_BF16 ? FMT_BF16 : FMT_F32);
+            store_float(out, i, fmt, round_fmt(r, fmt));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// ADD with broadcasting, src/ops/elementwise.rs:395-397 (+ :57-107, :138-145).
+// ---------------------------------------------------------------------------
+__global__ void add_kernel(int e, BroadcastDesc bd, const void* a, const void* b, void* out, int64_t count)
+{
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+        int64_t rem = i, ia = 0, ib = 0;
+        for (int dd = bd.rank - 1; dd >= 0; dd--) {
+            const int64_t k = rem % bd.out_dims[dd];
+            rem /= bd.out_dims[dd];
+            ia += k * bd.a_strides[dd];
+            ib += k * bd.b_strides[dd];
+        }
+        if (e == E_I32) {
+            static_cast<int32_t*>(out)[i] =
+                int32_t(uint32_t(static_cast<const int32_t*>(a)[ia]) + uint32_t(static_cast<const int32_t*>(b)[ib]));
+        } else if (e == E_I64) {
+            static_cast<int64_t*>(out)[i] =
+                int64_t(uint64_t(static_cast<const int64_t*>(a)[ia]) + uint64_t(static_cast<const int64_t*>(b)[ib]));
+        } else {
+            const int fmt = e == E_F16 ? FMT_F16 : (e == E_BF16 ? FMT_BF16 : FMT_F32);
+            const float r = round_fmt(load_float(a, ia, e) + load_float(b, ib, e), fmt);
+            store_float(out, i, fmt, r);
+        }
+    }
+}
+
+// RESCALE(a) + RESCALE(b) -> RESCALE, all elementwise with equal shapes.
+__global__ void residual_kernel(RescaleDev ra, RescaleDev rb, RescaleDev ro, const int8_t* a, const int8_t* b,
+                                int64_t count, int64_t channels, int8_t* out, uint32_t* err)
+{
+    uint32_t e = 0;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+        const int ch = int(i % channels);
+        const int ca = ra.per_channel ? ch : 0, cb = rb.per_channel ? ch : 0, co = ro.per_channel ? ch : 0;
+        const int32_t va = int32_t(rescale_value(a[i], ra.mult[ca], ra.shift[ca], ra, e));
+        const int32_t vb = int32_t(rescale_value(b[i], rb.mult[cb], rb.shift[cb], rb, e));
+        const int32_t s = int32_t(uint32_t(va) + uint32_t(vb));
+        out[i] = int8_t(rescale_value(s, ro.mult[co], ro.shift[co], ro, e));
+    }
+    report(err, e);
+}
+
+__global__ void residual_c4_kernel(RescaleDev ra, RescaleDev rb, RescaleDev ro, const int8_t* a, const int8_t* b,
+                                   int64_t count4, int64_t channels, int8_t* out, uint32_t* err)
+{
+    uint32_t e = 0;
+    for (int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; q < count4; q += int64_t(gridDim.x) * blockDim.x) {
+        const uint32_t wa = reinterpret_cast<const uint32_t*>(a)[q];
+        const uint32_t wb = reinterpret_cast<const uint32_t*>(b)[q];
+        const int ch0 = int((4 * q) % channels);
+        uint32_t packed = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int ch = ch0 + j;
+            const int ca = ra.per_channel ? ch : 0, cb = rb.per_channel ? ch : 0, co = ro.per_channel ? ch : 0;
+            const int32_t va = int32_t(rescale_value(int8_t(wa >> (8 * j)), ra.mult[ca], ra.shift[ca], ra, e));
+            const int32_t vb = int32_t(rescale_value(int8_t(wb >> (8 * j)), rb.mult[cb], rb.shift[cb], rb, e));
+            const int32_t s = int32_t(uint32_t(va) + uint32_t(vb));
+            packed |= (uint32_t(rescale_value(s, ro.mult[co], ro.shift[co], ro, e)) & 0xFFu) << (8 * j);
+        }
+        reinterpret_cast<uint32_t*>(out)[q] = packed;
+    }
+    report(err, e);
+}
+
+// ---------------------------------------------------------------------------
+// TRANSPOSE: output element i reads input at sum(index_d * stride_perm[d]).
+// ---------------------------------------------------------------------------
+struct TransposeArgs {
+    int32_t rank;
+    int64_t dims[6];
+    int64_t strides[6];
+};
+
+__global__ void transpose_kernel(const uint8_t* x, uint8_t* out, int esize, TransposeArgs t, int64_t count)
+{
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+        int64_t rem = i, src = 0;
+        for (int dd = t.rank - 1; dd >= 0; dd--) {
+            const int64_t k = rem % t.dims[dd];
+            rem /= t.dims[dd];
+            src += k * t.strides[dd];
+        }
+        for (int b = 0; b < esize; b++)
+            out[i * esize + b] = x[src * esize + b];
+    }
+}
+
+unsigned grid_for(int64_t n)
+{
+    const int64_t b = (n + 255) / 256;
+    return static_cast<unsigned>(b < 65536 ? (b < 1 ? 1 : b) : 65536);
+}
+
+}  // namespace
+
+bool depthwise_i8_supported(int kh, int kw, int c)
+{
+    const bool taps = (kh == 3 && kw == 3) || (kh == 1 && kw == 1) || (kh == 1 && kw == 3) || (kh == 3 && kw == 1) ||
+                      (kh == 2 && kw == 2);
+    return taps && c % 4 == 0;
+}
+
+void depthwise_i8(const DepthwiseDesc& d, const int8_t* x, const int8_t* w, void* out, uint32_t* err,
+                  hipStream_t stream)
+{
+    constexpr int PX = 4;
+    const int64_t total = int64_t(d.n) * d.oh * ((d.ow + PX - 1) / PX) * (d.c / 4);
+    if (total <= 0 || !depthwise_i8_supported(d.kh, d.kw, d.c))
+        return;
+    const dim3 grid(blocks_for(total, 256));
+    uint8_t* o = static_cast<uint8_t*>(out);
+    if (d.kh == 3 && d.kw == 3)
+        hipLaunchKernelGGL((dw_i8_kernel<3, 3, PX>), grid, dim3(256), 0, stream, d, x, w, o, err, total);
+    else if (d.kh == 1 && d.kw == 1)
+        hipLaunchKernelGGL((dw_i8_kernel<1, 1, PX>), grid, dim3(256), 0, stream, d, x, w, o, err, total);
+    else if (d.kh == 1 && d.kw == 3)
+        hipLaunchKernelGGL((dw_i8_kernel<1, 3, PX>), grid, dim3(256), 0, stream, d, x, w, o, err, total);
+    else if (d.kh == 3 && d.kw == 1)
+        hipLaunchKernelGGL((dw_i8_kernel<3, 1, PX>), grid, dim3(256), 0, stream, d, x, w, o, err, total);
+    else
+        hipLaunchKernelGGL((dw_i8_kernel<2, 2, PX>), grid, dim3(256), 0, stream, d, x, w, o, err, total);
+}
+
+void avg_pool2d(const PoolDesc& d, const void* x, void* out, uint32_t* err, hipStream_t stream)
+{
+    const int64_t total = int64_t(d.n) * d.oh * d.ow * d.c;
+    if (total <= 0)
+        return;
+    if (d.xe == E_I8 && d.c % 4 == 0) {
+        const int64_t t4 = total / 4;
+        hipLaunchKernelGGL(avg_pool_i8_c4_kernel, dim3(blocks_for(t4, 256)), dim3(256), 0, stream, d,
+                           static_cast<const int8_t*>(x), static_cast<int8_t*>(out), err, t4);
+    } else {
+        hipLaunchKernelGGL(avg_pool_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, d, x, out, err, total);
+    }
+}
+
+void rescale(const RescaleDev& rs, ElemCode xe, const void* x, int64_t count, void* out, uint32_t* err,
+             hipStream_t stream)
+{
+    if (count <= 0)
+        return;
+    if (xe == E_I8 && rs.out_bytes == 1 && count % 4 == 0 && (!rs.per_channel || rs.channels % 4 == 0)) {
+        hipLaunchKernelGGL(rescale_i8_c4_kernel, dim3(grid_for(count / 4)), dim3(256), 0, stream, rs,
+                           static_cast<const int8_t*>(x), count / 4, static_cast<int8_t*>(out), err);
+        return;
+    }
+    hipLaunchKernelGGL(rescale_kernel, dim3(grid_for(count)), dim3(256), 0, stream, rs, int(xe), x, count, out, err);
+}
+
+void clamp(ElemCode e, const void* x, int64_t count, int64_t ilo, int64_t ihi, float flo, float fhi, int nan_ignore,
+           void* out, hipStream_t stream)
+{
+    if (count > 0)
+        hipLaunchKernelGGL(clamp_kernel, dim3(grid_for(count)), dim3(256), 0, stream, int(e), x, count, ilo, ihi, flo,
+                           fhi, nan_ignore, out);
+}
+
+void add(ElemCode e, const BroadcastDesc& bd, const void* a, const void* b, void* out, int64_t count,
+         hipStream_t stream)
+{
+    if (count > 0)
+        hipLaunchKernelGGL(add_kernel, dim3(grid_for(count)), dim3(256), 0, stream, int(e), bd, a, b, out, count);
+}
+
+void residual_add_i8(const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro, const int8_t* a,
+                     const int8_t* b, int64_t count, int64_t channels, void* out, uint32_t* err,
+                     hipStream_t stream)
+{
+    if (count <= 0)
+        return;
+    if (count % 4 == 0 && channels % 4 == 0)
+        hipLaunchKernelGGL(residual_c4_kernel, dim3(grid_for(count / 4)), dim3(256), 0, stream, ra, rb, ro, a, b,
+                           count / 4, channels, static_cast<int8_t*>(out), err);
+    else
+        hipLaunchKernelGGL(residual_kernel, dim3(grid_for(count)), dim3(256), 0, stream, ra, rb, ro, a, b, count,
+                           channels, static_cast<int8_t*>(out), err);
+}
+
+void transpose(const void* x, void* out, int32_t esize, int32_t rank, const int64_t* out_dims,
+               const int64_t* in_strides_permuted, int64_t count, hipStream_t stream)
+{
+    if (count <= 0)
+        return;
+    TransposeArgs t{};
+    t.rank = rank;
+    for (int i = 0; i < rank; i++) {
+        t.dims[i] = out_dims[i];
+        t.strides[i] = in_strides_permuted[i];
+    }
+    hipLaunchKernelGGL(transpose_kernel, dim3(grid_for(count)), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(x), static_cast<uint8_t*>(out), esize, t, count);
+}
+
+}  // namespace kern
+}  // namespace tosa

@@ -1,0 +1,1346 @@
+// Operator evaluation on the MI355X path: the reference's per-operator
+// validation (same checks, same order, same error kinds) followed by a
+// kernel launch instead of a host loop. Dispatch mirrors src/ops/mod.rs:22-150
+// for the operators of this path; every other operator is rejected as
+// unsupported.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <optional>
+
+#include "exec.h"
+
+namespace tosa {
+
+using namespace kern;
+
+// ---------------------------------------------------------------------------
+// ExecState / ConstCache
+// ---------------------------------------------------------------------------
+TensorPtr ExecState::get(const std::string& name) const
+{
+    auto it = tensors.find(name);
+    if (it == tensors.end())
+        throw Error(ERR_TENSOR_NOT_FOUND, name);
+    return it->second;
+}
+
+const TensorDef* ExecState::find_def(const std::string& name) const
+{
+    auto it = defs.find(name);
+    return it == defs.end() ? nullptr : it->second;
+}
+
+static Shape shape_from_ir(const std::vector<int32_t>& s)
+{
+    Shape r;
+    r.reserve(s.size());
+    for (int32_t d : s)
+        r.push_back(d < 0 ? 0 : d);
+    return r;
+}
+
+StoragePtr ConstCache::get(const TensorDef& def)
+{
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = map_.find(&def);
+    if (it != map_.end())
+        return it->second;
+    const int64_t count = shape_count(shape_from_ir(def.shape));
+    StoragePtr s = def.has_data ? storage_from_raw_bytes(def.dtype, def.data.data(), def.data.size(), count)
+                                : storage_zeros(def.dtype, count);
+    map_[&def] = s;
+    return s;
+}
+
+TensorPtr ExecState::resolve(const std::string& name) const
+{
+    auto it = tensors.find(name);
+    if (it != tensors.end())
+        return it->second;
+    auto c = const_defs.find(name);
+    if (c == const_defs.end())
+        return nullptr;
+    try {
+        auto t = std::make_shared<Tensor>();
+        t->name = name;
+        t->shape = shape_from_ir(c->second->shape);
+        t->data = consts->get(*c->second);
+        return t;
+    } catch (const Error&) {
+        return nullptr;
+    }
+}
+
+namespace {
+
+TensorPtr make_tensor(const std::string& name, const Shape& shape, StoragePtr data)
+{
+    auto t = std::make_shared<Tensor>();
+    t->name = name;
+    t->shape = shape;
+    t->data = std::move(data);
+    return t;
+}
+
+TensorPtr new_output(const std::string& name, const Shape& shape, DType t)
+{
+    return make_tensor(name, shape, make_device_storage(t, shape_count(shape)));
+}
+
+// A tensor whose storage is computed on demand by `fill` (see Storage).
+TensorPtr virtual_output(const std::string& name, const Shape& shape, DType t, std::function<void(Storage&)> fill)
+{
+    auto s = std::make_shared<Storage>();
+    s->dtype = t;
+    s->count = shape_count(shape);
+    s->materialize = std::move(fill);
+    return make_tensor(name, shape, s);
+}
+
+// ---------------------------------------------------------------------------
+// Shared validation, src/ops/common.rs
+// ---------------------------------------------------------------------------
+void expect_operands(const Operator& op, const std::string& name, size_t in, size_t out)
+{
+    if (op.inputs.size() != in || op.outputs.size() != out)
+        throw invalid(name, "expected " + std::to_string(in) + " inputs and " + std::to_string(out) +
+                                " outputs, got " + std::to_string(op.inputs.size()) + " and " +
+                                std::to_string(op.outputs.size()));
+}
+
+void expect_rank(const std::string& op, const std::string& what, const Tensor& t, size_t rank)
+{
+    if (t.shape.size() != rank)
+        throw Error(ERR_SHAPE_MISMATCH,
+                    op + ": " + what + " must have rank " + std::to_string(rank) + ", got shape " + shape_str(t.shape));
+}
+
+TensorPtr single_value(const std::string& op, const std::string& what, TensorPtr t)
+{
+    expect_rank(op, what, *t, 1);
+    if (t->len() != 1)
+        throw Error(ERR_SHAPE_MISMATCH,
+                    op + ": " + what + " must have exactly one element, got shape " + shape_str(t->shape));
+    return t;
+}
+
+std::optional<DType> check_declared_output(const ExecState& st, const std::string& op, const std::string& name,
+                                           const Shape& shape)
+{
+    const TensorDef* def = st.find_def(name);
+    if (!def)
+        return std::nullopt;
+    const bool static_shape = std::all_of(def->shape.begin(), def->shape.end(), [](int32_t d) { return d >= 0; });
+    if (static_shape) {
+        Shape declared(def->shape.begin(), def->shape.end());
+        if (declared != shape)
+            throw Error(ERR_SHAPE_MISMATCH, op + ": output shape " + shape_str(shape) + " does not match declared shape " +
+                                                shape_str(declared));
+    }
+    return def->dtype;
+}
+
+// finish() of the element-wise and data-layout operators: declared shape and
+// dtype must match the result.
+void check_finish(const ExecState& st, const std::string& op, const std::string& out, const Shape& shape, DType t)
+{
+    auto d = check_declared_output(st, op, out, shape);
+    if (d && *d != t)
+        throw Error(ERR_DTYPE_MISMATCH,
+                    op + ": output dtype " + dtype_name(*d) + " should be " + dtype_name(t));
+}
+
+bool is_fp8(DType t) { return t == DT_FP8E4M3 || t == DT_FP8E5M2; }
+
+ElemCode elem_code(DType t)
+{
+    switch (t) {
+    case DT_BOOL: return E_U8;
+    case DT_INT4:
+    case DT_INT8: return E_I8;
+    case DT_INT16: return E_I16;
+    case DT_INT32: return E_I32;
+    case DT_INT48:
+    case DT_INT64:
+    case DT_SHAPE: return E_I64;
+    case DT_FP32: return E_F32;
+    case DT_FP16: return E_F16;
+    case DT_BF16: return E_BF16;
+    case DT_FP8E4M3: return E_FP8E4M3;
+    case DT_FP8E5M2: return E_FP8E5M2;
+    default: throw Error(ERR_DTYPE_MISMATCH, std::string("no device representation for ") + dtype_name(t));
+    }
+}
+
+int32_t fmt_code(DType t)
+{
+    switch (t) {
+    case DT_FP16: return FMT_F16;
+    case DT_BF16: return FMT_BF16;
+    case DT_FP8E4M3: return FMT_FP8E4M3;
+    case DT_FP8E5M2: return FMT_FP8E5M2;
+    default: return FMT_F32;
+    }
+}
+
+std::pair<int64_t, int64_t> int_range(DType t)
+{
+    switch (t) {
+    case DT_INT4: return {-8, 7};
+    case DT_INT8: return {-128, 127};
+    case DT_INT16: return {-32768, 32767};
+    case DT_INT32: return {INT32_MIN, INT32_MAX};
+    case DT_INT48: return {-(int64_t(1) << 47), (int64_t(1) << 47) - 1};
+    default: return {INT64_MIN, INT64_MAX};
+    }
+}
+
+// Device copy of a host-computed array, cached on `owner` under `key`.
+StoragePtr cached_aux(Storage& owner, int kind, const std::function<StoragePtr()>& make)
+{
+    if (owner.aux && owner.aux_kind == kind)
+        return owner.aux;
+    owner.aux = make();
+    owner.aux_kind = kind;
+    return owner.aux;
+}
+
+enum AuxKind { AUX_WSUM = 1, AUX_F32 = 2, AUX_RESCALE = 3 };
+
+// ---------------------------------------------------------------------------
+// RESCALE preparation: every check of eval_rescale (src/ops/type_conv.rs:
+// 111-170) plus the host-side parameter check that apply_scale_32/16 would
+// fail on (multiplier < 0, shift outside [2, 62]).
+// ---------------------------------------------------------------------------
+int bit_width(DType t) { return t == DT_INT8 ? 8 : t == DT_INT16 ? 16 : t == DT_INT32 ? 32 : 48; }
+
+struct RescalePrep {
+    DType in_t, out_t;
+    Shape shape;
+    RescaleDev rs;
+    StoragePtr params;  // [mult(channels) | shift(channels)] int32 on device
+};
+
+RescalePrep prepare_rescale(const ExecState& st, const Operator& op, const Tensor& input, TensorPtr multiplier,
+                            TensorPtr shift, TensorPtr in_zp, TensorPtr out_zp)
+{
+    const std::string OP = "RESCALE";
+    const OpAttribute& a = op.attr;
+    RescalePrep p;
+    p.shape = input.shape;
+    p.in_t = input.dtype();
+    p.out_t = check_declared_output(st, OP, op.outputs[0], p.shape).value_or(DT_INT32);
+    const DType in_t = p.in_t, out_t = p.out_t;
+    const bool in_ok = in_t == DT_INT8 || in_t == DT_INT16 || in_t == DT_INT32 || in_t == DT_INT48;
+    const bool out_ok = out_t == DT_INT8 || out_t == DT_INT16 || out_t == DT_INT32;
+    if (!in_ok || !out_ok)
+        throw Error(ERR_DTYPE_MISMATCH,
+                    OP + ": unsupported types " + dtype_name(in_t) + " -> " + dtype_name(out_t));
+    if (a.rounding_mode == ROUND_UNKNOWN)
+        throw invalid(OP, "unsupported rounding mode");
+    if (a.scale32 && in_t == DT_INT48)
+        throw invalid(OP, "scale32 is not allowed for INT48 input");
+    if (!a.scale32 && a.rounding_mode == ROUND_DOUBLE)
+        throw invalid(OP, "double rounding requires scale32");
+    const bool has32 = in_t == DT_INT32 || in_t == DT_INT48 || out_t == DT_INT32;
+    if ((a.input_unsigned && a.output_unsigned) || ((a.input_unsigned || a.output_unsigned) && has32))
+        throw invalid(OP, "invalid combination of input_unsigned/output_unsigned and types");
+    const DType want_m = a.scale32 ? DT_INT32 : DT_INT16;
+    if (multiplier->dtype() != want_m || shift->dtype() != DT_INT8)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": multiplier must be " + dtype_name(want_m) + " and shift INT8, got " +
+                                            dtype_name(multiplier->dtype()) + "/" + dtype_name(shift->dtype()));
+    if (in_zp->dtype() != in_t || out_zp->dtype() != out_t || in_zp->len() != 1 || out_zp->len() != 1)
+        throw invalid(OP, "zero points must be single elements of the input/output types");
+    int64_t channels = 1;
+    if (a.per_channel) {
+        if (p.shape.empty())
+            throw invalid(OP, "per_channel requires rank >= 1");
+        channels = p.shape.back();
+    }
+    if (multiplier->len() != channels || shift->len() != channels)
+        throw invalid(OP, "multiplier and shift must have " + std::to_string(channels) + " elements");
+    auto extend = [](DType t, int64_t v, bool u) { return u ? (v & ((int64_t(1) << bit_width(t)) - 1)) : v; };
+    const int64_t izp = extend(in_t, int_values(*in_zp)[0], a.input_unsigned);
+    const int64_t ozp = extend(out_t, int_values(*out_zp)[0], a.output_unsigned);
+    auto zp_ok = [](DType t, int64_t zp, bool u) { return t == DT_INT8 || zp == 0 || (t == DT_INT16 && u && zp == 32768); };
+    if (!zp_ok(in_t, izp, a.input_unsigned) || !zp_ok(out_t, ozp, a.output_unsigned))
+        throw invalid(OP, "zero point not allowed for this type");
+
+    // Widened multiplier and shift, cached with the multiplier tensor (for
+    // CONST operands: once per graph). The key includes the shift storage.
+    Storage& ms = *multiplier->data;
+    const Storage* shift_key = shift->data.get();
+    std::vector<int64_t> mv = int_values(*multiplier), sv = int_values(*shift);
+    if (shape_count(p.shape) > 0 && a.rounding_mode != ROUND_INEXACT) {
+        for (int64_t c = 0; c < channels; c++) {
+            const int64_t m = a.scale32 ? int64_t(int32_t(mv[c])) : int64_t(int16_t(mv[c]));
+            const int64_t s = int32_t(sv[c]);
+            if (m < 0 || s < 2 || s > 62)
+                throw Error(ERR_GRAPH, std::string(a.scale32 ? "apply_scale_32" : "apply_scale_16") +
+                                           ": invalid multiplier " + std::to_string(m) + " or shift " +
+                                           std::to_string(s));
+        }
+    }
+    if (!(ms.aux && ms.aux_kind == AUX_RESCALE && ms.aux->aux.get() == shift_key)) {
+        std::vector<int32_t> host(2 * channels);
+        for (int64_t c = 0; c < channels; c++) {
+            host[c] = int32_t(mv[c]);
+            host[channels + c] = int32_t(sv[c]);
+        }
+        auto params = make_host_storage(DT_INT32, 2 * channels, host.data());
+        // Remember which shift tensor these parameters were built from (a
+        // non-owning marker: the pointer is only compared).
+        params->aux = std::shared_ptr<Storage>(std::shared_ptr<Storage>(), const_cast<Storage*>(shift_key));
+        ms.aux = params;
+        ms.aux_kind = AUX_RESCALE;
+    }
+    p.params = ms.aux;
+    const int32_t* dp = static_cast<const int32_t*>(p.params->device_in());
+    RescaleDev& r = p.rs;
+    r.mult = dp;
+    r.shift = dp + channels;
+    r.channels = int32_t(channels);
+    r.per_channel = a.per_channel;
+    r.scale32 = a.scale32;
+    r.rounding = int32_t(a.rounding_mode);
+    r.in_bits = bit_width(in_t);
+    r.in_unsigned = a.input_unsigned;
+    r.in_zp = izp;
+    r.out_zp = ozp;
+    if (a.output_unsigned) {
+        r.lo = 0;
+        r.hi = (int64_t(1) << bit_width(out_t)) - 1;
+    } else {
+        auto [lo, hi] = int_range(out_t);
+        r.lo = lo;
+        r.hi = hi;
+    }
+    r.out_bytes = int32_t(dtype_size(out_t));
+    return p;
+}
+
+// Bounds of CLAMP, src/ops/elementwise.rs:314-343, for integer data.
+struct ClampPrep {
+    int64_t lo, hi;
+};
+
+ClampPrep prepare_clamp_int(const ExecState& st, const Operator& op, const Tensor& input)
+{
+    const std::string OP = "CLAMP";
+    if (op.attr.kind != AttrKind::Clamp)
+        throw invalid(OP, "missing attribute");
+    if (op.attr.nan_mode == NAN_UNKNOWN)
+        throw invalid(OP, "nan_mode must be PROPAGATE or IGNORE");
+    const DType t = input.dtype();
+    StoragePtr mn, mx;
+    try {
+        mn = storage_from_raw_bytes(t, op.attr.min_val.data(), op.attr.min_val.size(), 1);
+        mx = storage_from_raw_bytes(t, op.attr.max_val.data(), op.attr.max_val.size(), 1);
+    } catch (const Error&) {
+        throw invalid(OP, "malformed min/max");
+    }
+    expect_operands(op, OP, 1, 1);
+    if (t != DT_INT8 && t != DT_INT16)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported dtype " + dtype_name(t));
+    Tensor a, b;
+    a.data = mn;
+    b.data = mx;
+    ClampPrep c{int_values(a)[0], int_values(b)[0]};
+    if (c.hi < c.lo)
+        throw invalid(OP, "max_val must not be smaller than min_val");
+    check_finish(st, OP, op.outputs[0], input.shape, t);
+    return c;
+}
+
+// The RESCALE (and CLAMP) that follow an int32 producer, prepared for a
+// fused epilogue; nullopt when the chain cannot be fused.
+struct FusedTail {
+    const Operator* rop = nullptr;
+    const Operator* cop = nullptr;
+    RescalePrep rp;
+};
+
+std::optional<FusedTail> plan_tail(const ExecState& st, size_t head, const Shape& shape)
+{
+    if (!st.opts.fusion || !st.plan)
+        return std::nullopt;
+    const int j = st.plan->rescale_after[head];
+    if (j < 0)
+        return std::nullopt;
+    const Operator& rop = st.block->operators[j];
+    if (rop.attr.kind != AttrKind::Rescale || rop.inputs.size() != 5 || rop.outputs.size() != 1)
+        return std::nullopt;
+    TensorPtr ops[4];
+    for (int i = 0; i < 4; i++)
+        if (!(ops[i] = st.resolve(rop.inputs[1 + i])))
+            return std::nullopt;
+    Tensor tmp;
+    tmp.name = rop.inputs[0];
+    tmp.shape = shape;
+    tmp.data = std::make_shared<Storage>();
+    tmp.data->dtype = DT_INT32;
+    tmp.data->count = shape_count(shape);
+    FusedTail f;
+    f.rop = &rop;
+    try {
+        f.rp = prepare_rescale(st, rop, tmp, ops[0], ops[1], ops[2], ops[3]);
+    } catch (const Error&) {
+        return std::nullopt;
+    }
+    const int k = st.plan->clamp_after[j];
+    if (k >= 0) {
+        const Operator& cop = st.block->operators[k];
+        Tensor rt;
+        rt.shape = shape;
+        rt.data = std::make_shared<Storage>();
+        rt.data->dtype = f.rp.out_t;
+        rt.data->count = shape_count(shape);
+        try {
+            if (!cop.inputs.empty() && cop.inputs[0] == rop.outputs[0]) {
+                ClampPrep c = prepare_clamp_int(st, cop, rt);
+                f.cop = &cop;
+                f.rp.rs.has_clamp = 1;
+                f.rp.rs.clamp_lo = c.lo;
+                f.rp.rs.clamp_hi = c.hi;
+            }
+        } catch (const Error&) {
+            f.cop = nullptr;
+        }
+    }
+    return f;
+}
+
+// Register the outputs of a fused chain: the head's int32 result and (when
+// a CLAMP follows) the RESCALE result become virtual tensors recomputed on
+// demand; the last output is the one the fused kernel wrote.
+void finish_fused(ExecState& st, const std::string& head_out, const Shape& shape, const FusedTail& f,
+                  const TensorPtr& final_out, std::function<void(Storage&)> head_fill)
+{
+    auto head = virtual_output(head_out, shape, DT_INT32, std::move(head_fill));
+    st.set(head);
+    if (f.cop) {
+        RescalePrep rp = f.rp;
+        rp.rs.has_clamp = 0;
+        auto src = head;
+        auto mid = virtual_output(f.rop->outputs[0], shape, rp.out_t, [src, rp](Storage& out) {
+            Stream& s = thread_stream();
+            const void* x = src->data->device_in();
+            kern::rescale(rp.rs, E_I32, x, out.count, out.device_out(), s.err, s.s);
+        });
+        st.pending[f.rop->outputs[0]] = mid;
+        st.pending[f.cop->outputs[0]] = make_tensor(f.cop->outputs[0], shape, final_out->data);
+    } else {
+        st.pending[f.rop->outputs[0]] = make_tensor(f.rop->outputs[0], shape, final_out->data);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// CONST, CONST_SHAPE, IDENTITY (src/ops/data_nodes.rs:6-37)
+// ---------------------------------------------------------------------------
+void eval_const(ExecState& st, const Operator& op)
+{
+    if (op.outputs.empty())
+        throw Error(ERR_GRAPH, "CONST op has no output");
+    const std::string& out = op.outputs[0];
+    const TensorDef* def = st.find_def(out);
+    if (!def)
+        throw Error(ERR_TENSOR_NOT_FOUND, out);
+    st.set(make_tensor(out, shape_from_ir(def->shape), st.consts->get(*def)));
+}
+
+void eval_identity(ExecState& st, const Operator& op)
+{
+    if (op.inputs.empty())
+        throw Error(ERR_GRAPH, "IDENTITY op has no input");
+    if (op.outputs.empty())
+        throw Error(ERR_GRAPH, "IDENTITY op has no output");
+    auto in = st.get(op.inputs[0]);
+    st.set(make_tensor(op.outputs[0], in->shape, in->data));
+}
+
+// ---------------------------------------------------------------------------
+// RESHAPE, TRANSPOSE (src/ops/data_layout.rs:163-177, :246-273)
+// ---------------------------------------------------------------------------
+void eval_reshape(ExecState& st, const Operator& op)
+{
+    const std::string OP = "RESHAPE";
+    expect_operands(op, OP, 2, 1);
+    auto in = st.get(op.inputs[0]);
+    auto sh = st.get(op.inputs[1]);
+    if (!dtype_is_int(sh->dtype()) && sh->dtype() != DT_SHAPE)
+        throw invalid(OP, "operand '" + op.inputs[1] + "' must be a shape, got " + dtype_name(sh->dtype()));
+    std::vector<int64_t> ns = int_values(*sh);
+    for (int64_t d : ns)
+        if (d < 0)
+            throw invalid(OP, "shape " + shape_str(ns) + " must be non-negative");
+    Shape out(ns.begin(), ns.end());
+    if (shape_count(out) != shape_count(in->shape))
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": cannot reshape " + shape_str(in->shape) + " to " + shape_str(out));
+    check_finish(st, OP, op.outputs[0], out, in->dtype());
+    st.set(make_tensor(op.outputs[0], out, in->data));  // same elements, no copy
+}
+
+void eval_transpose(ExecState& st, const Operator& op)
+{
+    const std::string OP = "TRANSPOSE";
+    if (op.attr.kind != AttrKind::Transpose)
+        throw invalid(OP, "missing attribute");
+    expect_operands(op, OP, 1, 1);
+    auto in = st.get(op.inputs[0]);
+    if (in->shape.empty())
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": input must have rank at least 1");
+    const size_t rank = in->shape.size();
+    const auto& perms = op.attr.perms;
+    std::vector<bool> used(rank, false);
+    for (int32_t p : perms) {
+        if (p < 0 || size_t(p) >= rank || used[p])
+            throw invalid(OP, "perms must be a permutation of 0.." + std::to_string(rank));
+        used[p] = true;
+    }
+    if (perms.size() != rank)
+        throw invalid(OP, "perms must have " + std::to_string(rank) + " entries");
+    Shape out(rank);
+    std::vector<int64_t> strides(rank, 1), perm_strides(rank);
+    for (int d = int(rank) - 2; d >= 0; d--)
+        strides[d] = strides[d + 1] * in->shape[d + 1];
+    for (size_t d = 0; d < rank; d++) {
+        out[d] = in->shape[perms[d]];
+        perm_strides[d] = strides[perms[d]];
+    }
+    check_finish(st, OP, op.outputs[0], out, in->dtype());
+    if (rank > 6)
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": rank above 6");
+    auto o = new_output(op.outputs[0], out, in->dtype());
+    const int64_t n = shape_count(out);
+    if (n > 0)
+        kern::transpose(in->data->device_in(), o->data->device_out(), int32_t(dtype_size(in->dtype())), int32_t(rank),
+                        out.data(), perm_strides.data(), n, st.s());
+    st.set(o);
+}
+
+// ---------------------------------------------------------------------------
+// CONV2D / DEPTHWISE_CONV2D (src/ops/conv.rs:398-524)
+// ---------------------------------------------------------------------------
+struct ConvGeom {
+    int64_t n, ih, iw, ic, oc, m, kh, kw, oh, ow;
+    int64_t pt, pl, sy, sx, dy, dx;
+    Shape out_shape;
+};
+
+int64_t output_extent(const std::string& op, int64_t in, int32_t pb, int32_t pa, int64_t k, int32_t d, int32_t s)
+{
+    const int64_t full = in - 1 + pb + pa - (k - 1) * d;
+    if (full % s != 0)
+        throw invalid(op, "parameters must yield exact integer output dimensions");
+    const int64_t out = full / s + 1;
+    if (out < 1)
+        throw invalid(op, "output dimension " + std::to_string(out) + " must be positive");
+    return out;
+}
+
+void check_conv_attributes(const std::string& op, const OpAttribute& a)
+{
+    if (a.pad.size() != 4 || a.stride.size() != 2 || a.dilation.size() != 2)
+        throw invalid(op, "pad must have 4 elements, stride and dilation 2");
+    for (int32_t p : a.pad)
+        if (p < 0)
+            throw invalid(op, "pad must be non-negative");
+    for (int32_t s : a.stride)
+        if (s < 1)
+            throw invalid(op, "stride must be at least 1");
+    for (int32_t d : a.dilation)
+        if (d < 1)
+            throw invalid(op, "dilation must be at least 1");
+}
+
+ConvGeom conv_geometry(const std::string& op, bool depthwise, const Tensor& in, const Tensor& w, const OpAttribute& a)
+{
+    expect_rank(op, "input", in, 4);
+    expect_rank(op, "weight", w, 4);
+    check_conv_attributes(op, a);
+    ConvGeom g{};
+    g.n = in.shape[0];
+    g.ih = in.shape[1];
+    g.iw = in.shape[2];
+    g.ic = in.shape[3];
+    if (depthwise) {
+        g.kh = w.shape[0];
+        g.kw = w.shape[1];
+        if (w.shape[2] != g.ic)
+            throw Error(ERR_SHAPE_MISMATCH, op + ": weight channels " + std::to_string(w.shape[2]) +
+                                                " != input channels " + std::to_string(g.ic));
+        g.m = w.shape[3];
+        g.oc = g.ic * g.m;
+    } else {
+        if (w.shape[3] != g.ic)
+            throw Error(ERR_SHAPE_MISMATCH, op + ": weight input channels " + std::to_string(w.shape[3]) +
+                                                " != input channels " + std::to_string(g.ic));
+        g.oc = w.shape[0];
+        g.kh = w.shape[1];
+        g.kw = w.shape[2];
+        g.m = 1;
+    }
+    g.oh = output_extent(op, g.ih, a.pad[0], a.pad[1], g.kh, a.dilation[0], a.stride[0]);
+    g.ow = output_extent(op, g.iw, a.pad[2], a.pad[3], g.kw, a.dilation[1], a.stride[1]);
+    g.pt = a.pad[0];
+    g.pl = a.pad[2];
+    g.sy = a.stride[0];
+    g.sx = a.stride[1];
+    g.dy = a.dilation[0];
+    g.dx = a.dilation[1];
+    g.out_shape = {g.n, g.oh, g.ow, g.oc};
+    return g;
+}
+
+bool conv2d_types(DType i, DType w, DType acc, DType out)
+{
+    auto fp = [](DType t, std::initializer_list<DType> ok) {
+        if (is_fp8(t))
+            return true;
+        for (DType o : ok)
+            if (o == t)
+                return true;
+        return false;
+    };
+    if (i == DT_INT8 && (w == DT_INT8 || w == DT_INT4) && acc == DT_INT32 && out == DT_INT32)
+        return true;
+    if (i == DT_INT16 && w == DT_INT8 && acc == DT_INT48 && out == DT_INT48)
+        return true;
+    if (acc == DT_FP32 && out == DT_FP32)
+        return fp(i, {DT_FP16, DT_BF16, DT_FP32}) && fp(w, {DT_FP16, DT_BF16, DT_FP32});
+    if ((acc == DT_FP16 || acc == DT_FP32) && out == DT_FP16)
+        return fp(i, {DT_FP16}) && fp(w, {DT_FP16});
+    if ((acc == DT_BF16 || acc == DT_FP32) && out == DT_BF16)
+        return fp(i, {DT_BF16}) && fp(w, {DT_BF16});
+    return false;
+}
+
+bool standard_types(DType i, DType w, DType acc, DType out)
+{
+    if (i == DT_INT8 && (w == DT_INT8 || w == DT_INT4) && acc == DT_INT32 && out == DT_INT32)
+        return true;
+    if (i == DT_INT16 && w == DT_INT8 && acc == DT_INT48 && out == DT_INT48)
+        return true;
+    if (i == DT_FP16 && w == DT_FP16 && (acc == DT_FP16 || acc == DT_FP32) && out == DT_FP16)
+        return true;
+    if (i == DT_BF16 && w == DT_BF16 && acc == DT_FP32 && out == DT_BF16)
+        return true;
+    if (i == DT_FP32 && w == DT_FP32 && acc == DT_FP32 && out == DT_FP32)
+        return true;
+    if ((i == DT_FP8E4M3 && w == DT_FP8E4M3) || (i == DT_FP8E5M2 && w == DT_FP8E5M2))
+        return (acc == DT_FP16 && out == DT_FP16) || (acc == DT_FP32 && out == DT_FP32);
+    return false;
+}
+
+AccKind float_acc(DType acc) { return acc == DT_FP16 ? ACC_F16 : (acc == DT_BF16 ? ACC_BF16 : ACC_F32); }
+
+void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
+{
+    const std::string OP = depthwise ? "DEPTHWISE_CONV2D" : "CONV2D";
+    if (op.attr.kind != (depthwise ? AttrKind::DepthwiseConv2d : AttrKind::Conv2d))
+        throw invalid(OP, "missing attribute");
+    expect_operands(op, OP, 5, 1);
+    auto input = st.get(op.inputs[0]);
+    auto weight = st.get(op.inputs[1]);
+    auto bias = st.get(op.inputs[2]);
+    auto in_zp = single_value(OP, "input_zp", st.get(op.inputs[3]));
+    auto w_zp = single_value(OP, "weight_zp", st.get(op.inputs[4]));
+    const std::string& out_name = op.outputs[0];
+
+    expect_rank(OP, "bias", *bias, 1);
+    ConvGeom g = conv_geometry(OP, depthwise, *input, *weight, op.attr);
+    const int64_t bc = bias->shape[0];
+    if (bc != g.oc && bc != 1)
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": bias channels " + std::to_string(bc) +
+                                            " must be 1 or match output channels " + std::to_string(g.oc));
+    const DType in_t = input->dtype(), w_t = weight->dtype(), out_t = bias->dtype(), acc_t = op.attr.acc_type;
+    auto declared = check_declared_output(st, OP, out_name, g.out_shape);
+    if (declared && *declared != out_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": output dtype " + dtype_name(*declared) + " does not match bias dtype " +
+                                            dtype_name(out_t));
+    if (!(depthwise ? standard_types : conv2d_types)(in_t, w_t, acc_t, out_t))
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported types input=" + dtype_name(in_t) + " weight=" +
+                                            dtype_name(w_t) + " acc=" + dtype_name(acc_t) + " output=" +
+                                            dtype_name(out_t));
+    if (in_zp->dtype() != in_t || w_zp->dtype() != w_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": zero points must match input/weight dtypes");
+
+    const bool is_int = dtype_is_int(acc_t);
+    int64_t izp = 0, wzp = 0;
+    float fizp = 0.f, fwzp = 0.f;
+    if (is_int) {
+        izp = int_values(*in_zp)[0];
+        wzp = int_values(*w_zp)[0];
+        if (izp != 0 && in_t != DT_INT8)
+            throw invalid(OP, "input zero point must be zero for non-int8 input");
+        if (wzp != 0 && w_t != DT_INT8)
+            throw invalid(OP, "weight zero point must be zero for non-int8 weight");
+    } else {
+        fizp = float(float_values(*in_zp)[0]);
+        fwzp = float(float_values(*w_zp)[0]);
+        if (fizp != 0.0f || fwzp != 0.0f)
+            throw invalid(OP, "zero points must be zero for floating-point operands");
+    }
+
+    const int64_t count = shape_count(g.out_shape);
+    const int64_t K = g.kh * g.kw * (depthwise ? 1 : g.ic);
+    const bool i8 = is_int && acc_t == DT_INT32 && in_t == DT_INT8;
+    const bool mfma_int = i8 && !depthwise;
+    const bool dw_int = i8 && depthwise && g.m == 1 && depthwise_i8_supported(int(g.kh), int(g.kw), int(g.ic));
+    const bool mfma_float = !is_int && !depthwise && !st.opts.strict_float && acc_t == DT_FP32 &&
+                            ((in_t == DT_BF16 && w_t == DT_BF16) || (in_t == DT_FP16 && w_t == DT_FP16));
+
+    auto sizes_ok = [&]() {
+        return g.n * g.ih * g.iw * g.ic < (int64_t(1) << 31) && count < (int64_t(1) << 31) && K < (int64_t(1) << 30);
+    };
+
+    if ((mfma_int || dw_int) && sizes_ok()) {
+        // Per-channel weight sums, needed when the input zero point is not 0.
+        const int32_t* wsum = nullptr;
+        if (izp != 0 && mfma_int) {
+            Storage& ws = *weight->data;
+            auto sums = cached_aux(ws, AUX_WSUM, [&]() {
+                auto s = make_device_storage(DT_INT32, g.oc);
+                weight_sums_i8(static_cast<const int8_t*>(ws.device_in()), int32_t(g.oc), int32_t(K),
+                               static_cast<int32_t*>(s->device_out()), st.s());
+                return s;
+            });
+            wsum = static_cast<const int32_t*>(sums->device_in());
+        }
+        GemmDesc gd;
+        DepthwiseDesc dd{};
+        if (mfma_int) {
+            gd.is_conv = 1;
+            gd.elem = ELEM_I8;
+            gd.n = int32_t(g.n);
+            gd.ih = int32_t(g.ih);
+            gd.iw = int32_t(g.iw);
+            gd.ic = int32_t(g.ic);
+            gd.oc = int32_t(g.oc);
+            gd.kh = int32_t(g.kh);
+            gd.kw = int32_t(g.kw);
+            gd.oh = int32_t(g.oh);
+            gd.ow = int32_t(g.ow);
+            gd.pt = int32_t(g.pt);
+            gd.pl = int32_t(g.pl);
+            gd.sy = int32_t(g.sy);
+            gd.sx = int32_t(g.sx);
+            gd.dy = int32_t(g.dy);
+            gd.dx = int32_t(g.dx);
+            gd.zp_x = int32_t(izp);
+            gd.zp_w = int32_t(wzp);
+            gd.wsum = wsum;
+            gd.bias = bias->data->device_in();
+            gd.bias_len = int32_t(bc);
+        } else {
+            dd.n = int32_t(g.n);
+            dd.ih = int32_t(g.ih);
+            dd.iw = int32_t(g.iw);
+            dd.c = int32_t(g.ic);
+            dd.kh = int32_t(g.kh);
+            dd.kw = int32_t(g.kw);
+            dd.oh = int32_t(g.oh);
+            dd.ow = int32_t(g.ow);
+            dd.pt = int32_t(g.pt);
+            dd.pl = int32_t(g.pl);
+            dd.sy = int32_t(g.sy);
+            dd.sx = int32_t(g.sx);
+            dd.dy = int32_t(g.dy);
+            dd.dx = int32_t(g.dx);
+            dd.zp_x = int32_t(izp);
+            dd.zp_w = int32_t(wzp);
+            dd.bias = static_cast<const int32_t*>(bias->data->device_in());
+            dd.bias_len = int32_t(bc);
+        }
+        const void* x = input->data->device_in();
+        const void* w = weight->data->device_in();
+        // Keep the operands alive for a later recomputation of a fused-away
+        // int32 output.
+        auto launch = [gd, dd, mfma_int, x, w, input, weight, bias](void* out, const RescaleDev* rs, uint32_t* err,
+                                                                      hipStream_t s) {
+            if (mfma_int) {
+                GemmDesc d = gd;
+                if (rs) {
+                    d.epi = EPI_RESCALE;
+                    d.rs = *rs;
+                }
+                kern::gemm(d, x, w, out, err, s);
+            } else {
+                DepthwiseDesc d = dd;
+                if (rs) {
+                    d.epi = EPI_RESCALE;
+                    d.rs = *rs;
+                }
+                kern::depthwise_i8(d, static_cast<const int8_t*>(x), static_cast<const int8_t*>(w), out, err, s);
+            }
+        };
+        if (auto tail = plan_tail(st, index, g.out_shape)) {
+            const DType final_t = tail->rp.out_t;
+            auto fin = new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], g.out_shape, final_t);
+            if (count > 0)
+                launch(fin->data->device_out(), &tail->rp.rs, st.err(), st.s());
+            auto keep = tail->rp.params;
+            finish_fused(st, out_name, g.out_shape, *tail, fin, [launch, keep](Storage& o) {
+                Stream& s = thread_stream();
+                if (o.count > 0)
+                    launch(o.device_out(), nullptr, s.err, s.s);
+                else
+                    o.device_out();
+            });
+            return;
+        }
+        auto out = new_output(out_name, g.out_shape, DT_INT32);
+        void* od = out->data->device_out();
+        if (count > 0)
+            launch(od, nullptr, st.err(), st.s());
+        st.set(out);
+        return;
+    }
+
+    if (mfma_float && sizes_ok()) {
+        // Bias as f32 values, cached with the bias tensor.
+        Storage& bs = *bias->data;
+        auto bf = cached_aux(bs, AUX_F32, [&]() {
+            std::vector<double> v = float_values(*bias);
+            std::vector<float> f(v.begin(), v.end());
+            return make_host_storage(DT_FP32, int64_t(f.size()), f.data());
+        });
+        GemmDesc gd;
+        gd.is_conv = 1;
+        gd.elem = in_t == DT_BF16 ? ELEM_BF16 : ELEM_F16;
+        gd.n = int32_t(g.n);
+        gd.ih = int32_t(g.ih);
+        gd.iw = int32_t(g.iw);
+        gd.ic = int32_t(g.ic);
+        gd.oc = int32_t(g.oc);
+        gd.kh = int32_t(g.kh);
+        gd.kw = int32_t(g.kw);
+        gd.oh = int32_t(g.oh);
+        gd.ow = int32_t(g.ow);
+        gd.pt = int32_t(g.pt);
+        gd.pl = int32_t(g.pl);
+        gd.sy = int32_t(g.sy);
+        gd.sx = int32_t(g.sx);
+        gd.dy = int32_t(g.dy);
+        gd.dx = int32_t(g.dx);
+        gd.bias = bf->device_in();
+        gd.bias_len = int32_t(bc);
+        gd.epi = EPI_FLOAT;
+        gd.out_fmt = FloatFmt(fmt_code(out_t));
+        auto out = new_output(out_name, g.out_shape, out_t);
+        void* od = out->data->device_out();
+        if (count > 0)
+            kern::gemm(gd, input->data->device_in(), weight->data->device_in(), od, st.err(), st.s());
+        st.set(out);
+        return;
+    }
+
+    // Reference-order kernel for every other combination.
+    DirectConvDesc d{};
+    d.depthwise = depthwise;
+    d.n = int32_t(g.n);
+    d.ih = int32_t(g.ih);
+    d.iw = int32_t(g.iw);
+    d.c = int32_t(g.ic);
+    d.m = int32_t(g.m);
+    d.oc = int32_t(g.oc);
+    d.kh = int32_t(g.kh);
+    d.kw = int32_t(g.kw);
+    d.oh = int32_t(g.oh);
+    d.ow = int32_t(g.ow);
+    d.pt = int32_t(g.pt);
+    d.pl = int32_t(g.pl);
+    d.sy = int32_t(g.sy);
+    d.sx = int32_t(g.sx);
+    d.dy = int32_t(g.dy);
+    d.dx = int32_t(g.dx);
+    d.xe = elem_code(in_t);
+    d.we = elem_code(w_t);
+    d.be = elem_code(out_t);
+    d.oe = elem_code(out_t);
+    d.acc = is_int ? (acc_t == DT_INT32 ? ACC_I32 : ACC_I64) : float_acc(acc_t);
+    d.zp_x = izp;
+    d.zp_w = wzp;
+    d.fzp_x = fizp;
+    d.fzp_w = fwzp;
+    d.bias_len = int32_t(bc);
+    d.out_fmt = fmt_code(out_t);
+    auto out = new_output(out_name, g.out_shape, out_t);
+    void* od = out->data->device_out();
+    if (count > 0)
+        kern::direct_conv(d, input->data->device_in(), weight->data->device_in(), bias->data->device_in(), od, st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// MATMUL (src/ops/matmul.rs:98-178)
+// ---------------------------------------------------------------------------
+bool matmul_types(DType a, DType b, DType out)
+{
+    if (a == DT_INT8 && b == DT_INT8 && out == DT_INT32)
+        return true;
+    if (a == DT_INT16 && b == DT_INT16 && out == DT_INT48)
+        return true;
+    if (a == DT_FP16 && b == DT_FP16 && (out == DT_FP16 || out == DT_FP32))
+        return true;
+    if (a == DT_BF16 && b == DT_BF16 && out == DT_FP32)
+        return true;
+    if (a == DT_FP32 && b == DT_FP32 && out == DT_FP32)
+        return true;
+    if (out == DT_FP16 || out == DT_FP32)
+        return is_fp8(a) && is_fp8(b);
+    return false;
+}
+
+DType matmul_default_output(DType a)
+{
+    switch (a) {
+    case DT_INT8: return DT_INT32;
+    case DT_INT16: return DT_INT48;
+    case DT_FP16:
+    case DT_FP8E4M3:
+    case DT_FP8E5M2: return DT_FP16;
+    default: return DT_FP32;
+    }
+}
+
+void eval_matmul(ExecState& st, const Operator& op, size_t index)
+{
+    const std::string OP = "MATMUL";
+    expect_operands(op, OP, 4, 1);
+    auto a = st.get(op.inputs[0]);
+    auto b = st.get(op.inputs[1]);
+    auto a_zp = single_value(OP, "a_zp", st.get(op.inputs[2]));
+    auto b_zp = single_value(OP, "b_zp", st.get(op.inputs[3]));
+    const std::string& out_name = op.outputs[0];
+    expect_rank(OP, "a", *a, 3);
+    expect_rank(OP, "b", *b, 3);
+    const int64_t n = a->shape[0], h = a->shape[1], c = a->shape[2];
+    const int64_t bn = b->shape[0], bc = b->shape[1], w = b->shape[2];
+    if (bc != c || bn != n)
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": b shape " + shape_str(b->shape) + " incompatible with a shape " +
+                                            shape_str(a->shape));
+    const Shape out_shape = {n, h, w};
+    const DType a_t = a->dtype(), b_t = b->dtype();
+    const DType out_t = check_declared_output(st, OP, out_name, out_shape).value_or(matmul_default_output(a_t));
+    if (!matmul_types(a_t, b_t, out_t))
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported types a=" + dtype_name(a_t) + " b=" + dtype_name(b_t) +
+                                            " output=" + dtype_name(out_t));
+    if (a_zp->dtype() != a_t || b_zp->dtype() != b_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": zero points must match input dtypes");
+    const int64_t count = shape_count(out_shape);
+    const bool is_int = dtype_is_int(out_t);
+    int64_t azp = 0, bzp = 0;
+    if (is_int) {
+        azp = int_values(*a_zp)[0];
+        bzp = int_values(*b_zp)[0];
+        if ((azp != 0 && a_t != DT_INT8) || (bzp != 0 && b_t != DT_INT8))
+            throw invalid(OP, "zero points must be zero for non-int8 inputs");
+    } else {
+        if (float_values(*a_zp)[0] != 0.0 || float_values(*b_zp)[0] != 0.0)
+            throw invalid(OP, "zero points must be zero for floating-point inputs");
+    }
+    const bool small = n * h * c < (int64_t(1) << 31) && n * c * w < (int64_t(1) << 31) && count < (int64_t(1) << 31);
+    const bool mfma_int = out_t == DT_INT32 && small;
+    const bool mfma_float = !is_int && out_t == DT_FP32 && !st.opts.strict_float && small &&
+                            ((a_t == DT_BF16 && b_t == DT_BF16) || (a_t == DT_FP16 && b_t == DT_FP16));
+    if (mfma_int || mfma_float) {
+        GemmDesc gd;
+        gd.is_conv = 0;
+        gd.elem = mfma_int ? ELEM_I8 : (a_t == DT_BF16 ? ELEM_BF16 : ELEM_F16);
+        gd.batch = int32_t(n);
+        gd.h = int32_t(h);
+        gd.c = int32_t(c);
+        gd.w = int32_t(w);
+        gd.zp_x = int32_t(azp);
+        gd.zp_w = int32_t(bzp);
+        gd.epi = mfma_int ? EPI_I32 : EPI_FLOAT;
+        gd.out_fmt = FMT_F32;
+        const void* ad = a->data->device_in();
+        const void* bd = b->data->device_in();
+        if (mfma_int) {
+            if (auto tail = plan_tail(st, index, out_shape)) {
+                auto fin =
+                    new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], out_shape, tail->rp.out_t);
+                GemmDesc fd = gd;
+                fd.epi = EPI_RESCALE;
+                fd.rs = tail->rp.rs;
+                void* fo = fin->data->device_out();
+                if (count > 0)
+                    kern::gemm(fd, ad, bd, fo, st.err(), st.s());
+                auto keep = tail->rp.params;
+                finish_fused(st, out_name, out_shape, *tail, fin, [gd, ad, bd, a, b, keep](Storage& o) {
+                    Stream& s = thread_stream();
+                    void* od = o.device_out();
+                    if (o.count > 0)
+                        kern::gemm(gd, ad, bd, od, s.err, s.s);
+                });
+                return;
+            }
+        }
+        auto out = new_output(out_name, out_shape, out_t);
+        void* od = out->data->device_out();
+        if (count > 0)
+            kern::gemm(gd, ad, bd, od, st.err(), st.s());
+        st.set(out);
+        return;
+    }
+    DirectMatmulDesc d{};
+    d.batch = int32_t(n);
+    d.h = int32_t(h);
+    d.c = int32_t(c);
+    d.w = int32_t(w);
+    d.ae = elem_code(a_t);
+    d.be = elem_code(b_t);
+    d.oe = elem_code(out_t);
+    d.zp_a = azp;
+    d.zp_b = bzp;
+    if (is_int)
+        d.acc = out_t == DT_INT32 ? ACC_I32 : ACC_I64;
+    else
+        d.acc = out_t == DT_FP16 ? ACC_F16U : (out_t == DT_BF16 ? ACC_BF16U : ACC_F32);
+    d.out_fmt = fmt_code(out_t);
+    auto out = new_output(out_name, out_shape, out_t);
+    void* od = out->data->device_out();
+    if (count > 0)
+        kern::direct_matmul(d, a->data->device_in(), b->data->device_in(), od, st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// AVG_POOL2D (src/ops/pool.rs:17-105, :146-231)
+// ---------------------------------------------------------------------------
+void eval_avg_pool2d(ExecState& st, const Operator& op)
+{
+    const std::string OP = "AVG_POOL2D";
+    if (op.attr.kind != AttrKind::Pool2d)
+        throw invalid(OP, "missing attribute");
+    const auto& kernel = op.attr.kernel;
+    const auto& stride = op.attr.stride;
+    const auto& pad = op.attr.pad;
+    const DType acc_t = op.attr.acc_type;
+    expect_operands(op, OP, 3, 1);
+    auto input = st.get(op.inputs[0]);
+    auto izp = single_value(OP, "input_zp", st.get(op.inputs[1]));
+    auto ozp = single_value(OP, "output_zp", st.get(op.inputs[2]));
+    expect_rank(OP, "input", *input, 4);
+    if (pad.size() != 4 || kernel.size() != 2 || stride.size() != 2)
+        throw invalid(OP, "pad must have 4 elements, kernel and stride 2");
+    for (int32_t p : pad)
+        if (p < 0)
+            throw invalid(OP, "pad must be non-negative");
+    for (int32_t k : kernel)
+        if (k < 1)
+            throw invalid(OP, "kernel and stride must be at least 1");
+    for (int32_t s : stride)
+        if (s < 1)
+            throw invalid(OP, "kernel and stride must be at least 1");
+    if (pad[0] >= kernel[0] || pad[1] >= kernel[0] || pad[2] >= kernel[1] || pad[3] >= kernel[1])
+        throw invalid(OP, "pad must be smaller than kernel");
+    const int64_t n = input->shape[0], ih = input->shape[1], iw = input->shape[2], c = input->shape[3];
+    if (ih == 0 || iw == 0)
+        throw invalid(OP, "input height and width must be positive");
+    auto extent = [&](int64_t size, int32_t a, int32_t b, int32_t k, int32_t s) {
+        const int64_t full = size + a + b - k;
+        if (full < 0 || full % s != 0)
+            throw invalid(OP, "parameters must yield exact integer output dimensions");
+        return full / s + 1;
+    };
+    const int64_t oh = extent(ih, pad[0], pad[1], kernel[0], stride[0]);
+    const int64_t ow = extent(iw, pad[2], pad[3], kernel[1], stride[1]);
+    const Shape out_shape = {n, oh, ow, c};
+    const DType in_t = input->dtype();
+    auto declared = check_declared_output(st, OP, op.outputs[0], out_shape);
+    if (declared && *declared != in_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": output dtype " + dtype_name(*declared) + " must match input dtype " +
+                                            dtype_name(in_t));
+    const bool supported = ((in_t == DT_INT8 || in_t == DT_INT16) && acc_t == DT_INT32) ||
+                           (in_t == DT_FP16 && (acc_t == DT_FP16 || acc_t == DT_FP32)) ||
+                           (in_t == DT_BF16 && acc_t == DT_FP32) || (in_t == DT_FP32 && acc_t == DT_FP32) ||
+                           (is_fp8(in_t) && acc_t == DT_FP16);
+    if (!supported)
+        throw Error(ERR_DTYPE_MISMATCH,
+                    OP + ": unsupported types input=" + dtype_name(in_t) + " acc=" + dtype_name(acc_t));
+    if (izp->dtype() != in_t || ozp->dtype() != in_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": zero points must have the input dtype");
+    PoolDesc d{};
+    d.n = int32_t(n);
+    d.ih = int32_t(ih);
+    d.iw = int32_t(iw);
+    d.c = int32_t(c);
+    d.kh = kernel[0];
+    d.kw = kernel[1];
+    d.oh = int32_t(oh);
+    d.ow = int32_t(ow);
+    d.pt = pad[0];
+    d.pl = pad[2];
+    d.sy = stride[0];
+    d.sx = stride[1];
+    d.xe = elem_code(in_t);
+    if (dtype_is_int(in_t)) {
+        const int64_t iz = int_values(*izp)[0], oz = int_values(*ozp)[0];
+        if (in_t != DT_INT8 && (iz != 0 || oz != 0))
+            throw invalid(OP, "zero points must be zero for non-int8 data");
+        d.in_zp = iz;
+        d.out_zp = oz;
+        auto [lo, hi] = int_range(in_t);
+        d.lo = lo;
+        d.hi = hi;
+    } else {
+        if (float_values(*izp)[0] != 0.0 || float_values(*ozp)[0] != 0.0)
+            throw invalid(OP, "zero points must be zero for floating-point data");
+        d.acc_fmt = fmt_code(acc_t);
+        d.out_fmt = fmt_code(in_t);
+    }
+    auto out = new_output(op.outputs[0], out_shape, in_t);
+    void* od = out->data->device_out();
+    if (shape_count(out_shape) > 0)
+        kern::avg_pool2d(d, input->data->device_in(), od, st.err(), st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// RESCALE (src/ops/type_conv.rs:111-191)
+// ---------------------------------------------------------------------------
+// Recipe of a deferred RESCALE from int8 to int32 (a residual operand).
+struct RescaleRecipe {
+    TensorPtr src;
+    RescalePrep rp;
+};
+
+void eval_rescale(ExecState& st, const Operator& op, size_t index)
+{
+    const std::string OP = "RESCALE";
+    if (op.attr.kind != AttrKind::Rescale)
+        throw invalid(OP, "missing attribute");
+    expect_operands(op, OP, 5, 1);
+    auto input = st.get(op.inputs[0]);
+    auto mult = st.get(op.inputs[1]);
+    auto shift = st.get(op.inputs[2]);
+    auto izp = st.get(op.inputs[3]);
+    auto ozp = st.get(op.inputs[4]);
+    auto pend = st.pending.find(op.outputs[0]);
+    if (pend != st.pending.end()) {
+        // Produced by the fused kernel of the operator feeding this one; the
+        // same checks passed when that kernel was planned.
+        st.set(pend->second);
+        st.pending.erase(pend);
+        return;
+    }
+    RescalePrep p = prepare_rescale(st, op, *input, mult, shift, izp, ozp);
+    const int64_t count = shape_count(p.shape);
+    if (st.opts.fusion && st.plan && st.plan->residual_input[index] && p.in_t == DT_INT8 && p.out_t == DT_INT32) {
+        auto src = input;
+        auto out = virtual_output(op.outputs[0], p.shape, p.out_t, [src, p](Storage& o) {
+            Stream& s = thread_stream();
+            const void* x = src->data->device_in();
+            kern::rescale(p.rs, E_I8, x, o.count, o.device_out(), s.err, s.s);
+        });
+        auto recipe = std::make_shared<RescaleRecipe>();
+        recipe->src = input;
+        recipe->rp = p;
+        // The recipe rides on the virtual storage as an opaque aux entry.
+        out->data->aux = std::shared_ptr<Storage>(recipe, reinterpret_cast<Storage*>(recipe.get()));
+        out->data->aux_kind = 100;
+        st.set(out);
+        return;
+    }
+    auto out = new_output(op.outputs[0], p.shape, p.out_t);
+    void* od = out->data->device_out();
+    if (count > 0)
+        kern::rescale(p.rs, elem_code(p.in_t), input->data->device_in(), count, od, st.err(), st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// CLAMP (src/ops/elementwise.rs:314-343)
+// ---------------------------------------------------------------------------
+void eval_clamp(ExecState& st, const Operator& op)
+{
+    const std::string OP = "CLAMP";
+    if (op.attr.kind != AttrKind::Clamp)
+        throw invalid(OP, "missing attribute");
+    if (op.attr.nan_mode == NAN_UNKNOWN)
+        throw invalid(OP, "nan_mode must be PROPAGATE or IGNORE");
+    const DType t = st.get(op.inputs.empty() ? std::string() : op.inputs[0])->dtype();
+    StoragePtr mn, mx;
+    try {
+        mn = storage_from_raw_bytes(t, op.attr.min_val.data(), op.attr.min_val.size(), 1);
+        mx = storage_from_raw_bytes(t, op.attr.max_val.data(), op.attr.max_val.size(), 1);
+    } catch (const Error&) {
+        throw invalid(OP, "malformed min/max");
+    }
+    expect_operands(op, OP, 1, 1);
+    auto input = st.get(op.inputs[0]);
+    if (!(t == DT_FP16 || t == DT_BF16 || t == DT_FP32 || t == DT_INT8 || t == DT_INT16))
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported dtype " + dtype_name(t));
+    Tensor tmn, tmx;
+    tmn.data = mn;
+    tmx.data = mx;
+    int64_t ilo = 0, ihi = 0;
+    float flo = 0, fhi = 0;
+    if (dtype_is_int(t)) {
+        ilo = int_values(tmn)[0];
+        ihi = int_values(tmx)[0];
+        if (ihi < ilo)
+            throw invalid(OP, "max_val must not be smaller than min_val");
+    } else {
+        flo = float(float_values(tmn)[0]);
+        fhi = float(float_values(tmx)[0]);
+        if (std::isnan(flo) || std::isnan(fhi) || fhi < flo)
+            throw invalid(OP, "min_val/max_val must be ordered and not NaN");
+    }
+    check_finish(st, OP, op.outputs[0], input->shape, t);
+    auto pend = st.pending.find(op.outputs[0]);
+    if (pend != st.pending.end()) {
+        st.set(pend->second);
+        st.pending.erase(pend);
+        return;
+    }
+    auto out = new_output(op.outputs[0], input->shape, t);
+    void* od = out->data->device_out();
+    const int64_t count = shape_count(input->shape);
+    if (count > 0)
+        kern::clamp(elem_code(t), input->data->device_in(), count, ilo, ihi, flo, fhi,
+                    op.attr.nan_mode == NAN_IGNORE, od, st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// ADD (src/ops/elementwise.rs:57-107, :359-397)
+// ---------------------------------------------------------------------------
+void eval_add(ExecState& st, const Operator& op, size_t index)
+{
+    const std::string OP = "ADD";
+    expect_operands(op, OP, 2, 1);
+    auto a = st.get(op.inputs[0]);
+    auto b = st.get(op.inputs[1]);
+    if (a->dtype() != b->dtype())
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": input dtypes " + dtype_name(a->dtype()) + " and " +
+                                            dtype_name(b->dtype()) + " differ");
+    const size_t rank = a->shape.size();
+    if (b->shape.size() != rank)
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": operand ranks differ");
+    Shape out(rank);
+    for (size_t d = 0; d < rank; d++) {
+        int64_t dim = 1;
+        for (int64_t s : {a->shape[d], b->shape[d]}) {
+            if (s != 1) {
+                if (dim != 1 && dim != s)
+                    throw Error(ERR_BROADCAST, OP + ": shapes " + shape_str(a->shape) + " and " + shape_str(b->shape) +
+                                                   " are not broadcastable");
+                dim = s;
+            }
+        }
+        out[d] = dim;
+    }
+    const DType t = a->dtype();
+    if (!(t == DT_FP16 || t == DT_BF16 || t == DT_FP32 || t == DT_INT32 || t == DT_INT64))
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported dtype " + dtype_name(t));
+    check_finish(st, OP, op.outputs[0], out, t);
+    if (rank > 6)
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": rank above 6");
+    const int64_t count = shape_count(out);
+
+    // Quantised residual: ADD(RESCALE(int8), RESCALE(int8)) -> RESCALE(int8).
+    auto recipe_of = [](const TensorPtr& x) -> RescaleRecipe* {
+        if (x->data->is_virtual() && x->data->aux_kind == 100)
+            return reinterpret_cast<RescaleRecipe*>(x->data->aux.get());
+        return nullptr;
+    };
+    if (st.opts.fusion && st.plan && st.plan->residual_tail[index] >= 0 && t == DT_INT32 && a->shape == out &&
+        b->shape == out && !out.empty()) {
+        RescaleRecipe* ra = recipe_of(a);
+        RescaleRecipe* rb = recipe_of(b);
+        if (ra && rb) {
+            const Operator& rop = st.block->operators[st.plan->residual_tail[index]];
+            TensorPtr ops[4];
+            bool ok = rop.attr.kind == AttrKind::Rescale && rop.inputs.size() == 5 && rop.outputs.size() == 1;
+            for (int i = 0; ok && i < 4; i++)
+                ok = (ops[i] = st.resolve(rop.inputs[1 + i])) != nullptr;
+            std::optional<RescalePrep> tail;
+            if (ok) {
+                Tensor tmp;
+                tmp.shape = out;
+                tmp.data = std::make_shared<Storage>();
+                tmp.data->dtype = DT_INT32;
+                tmp.data->count = count;
+                try {
+                    tail = prepare_rescale(st, rop, tmp, ops[0], ops[1], ops[2], ops[3]);
+                } catch (const Error&) {
+                    tail.reset();
+                }
+            }
+            if (tail && tail->out_t == DT_INT8) {
+                auto fin = new_output(rop.outputs[0], out, DT_INT8);
+                void* fo = fin->data->device_out();
+                kern::residual_add_i8(ra->rp.rs, rb->rp.rs, tail->rs,
+                                      static_cast<const int8_t*>(ra->src->data->device_in()),
+                                      static_cast<const int8_t*>(rb->src->data->device_in()), count, out.back(), fo,
+                                      st.err(), st.s());
+                BroadcastDesc bd{};
+                bd.rank = int32_t(rank);
+                int64_t s = 1;
+                for (int d = int(rank) - 1; d >= 0; d--) {
+                    bd.out_dims[d] = out[d];
+                    bd.a_strides[d] = s;
+                    bd.b_strides[d] = s;
+                    s *= out[d];
+                }
+                auto keep = tail->params;
+                auto sum = virtual_output(op.outputs[0], out, DT_INT32, [a, b, bd, keep](Storage& o) {
+                    Stream& s = thread_stream();
+                    const void* ad = a->data->device_in();
+                    const void* bdp = b->data->device_in();
+                    kern::add(E_I32, bd, ad, bdp, o.device_out(), o.count, s.s);
+                });
+                st.set(sum);
+                st.pending[rop.outputs[0]] = fin;
+                return;
+            }
+        }
+    }
+
+    BroadcastDesc bd{};
+    bd.rank = int32_t(rank);
+    int64_t sa = 1, sb = 1;
+    for (int d = int(rank) - 1; d >= 0; d--) {
+        bd.out_dims[d] = out[d];
+        bd.a_strides[d] = a->shape[d] == 1 ? 0 : sa;
+        bd.b_strides[d] = b->shape[d] == 1 ? 0 : sb;
+        sa *= a->shape[d];
+        sb *= b->shape[d];
+    }
+    auto o = new_output(op.outputs[0], out, t);
+    void* od = o->data->device_out();
+    if (count > 0)
+        kern::add(elem_code(t), bd, a->data->device_in(), b->data->device_in(), od, count, st.s());
+    st.set(o);
+}
+
+}  // namespace
+
+void dispatch(ExecState& st, const Operator& op, size_t index)
+{
+    switch (op.op) {
+    case OP_CONST:
+    case OP_CONST_SHAPE: eval_const(st, op); return;
+    case OP_IDENTITY: eval_identity(st, op); return;
+    case OP_RESHAPE: eval_reshape(st, op); return;
+    case OP_TRANSPOSE: eval_transpose(st, op); return;
+    case OP_CONV2D: eval_conv(st, op, index, false); return;
+    case OP_DEPTHWISE_CONV2D: eval_conv(st, op, index, true); return;
+    case OP_MATMUL: eval_matmul(st, op, index); return;
+    case OP_AVG_POOL2D: eval_avg_pool2d(st, op); return;
+    case OP_RESCALE: eval_rescale(st, op, index); return;
+    case OP_CLAMP: eval_clamp(st, op); return;
+    case OP_ADD: eval_add(st, op, index); return;
+    default: break;
+    }
+    if (op.op > OP_LAST)
+        throw Error(ERR_UNSUPPORTED_OP, "op code " + std::to_string(op.op));
+    throw Error(ERR_UNSUPPORTED_OP, std::string(op_name(op.op)) + " (not part of the MI355X execution path)");
+}
+
+}  // namespace tosa
