@@ -1,0 +1,232 @@
+"""Benchmark of the MI355X TOSA execution path.
+
+Headline workload (one "step" = one run of the graph through the C ABI on
+device-resident input): int8 CONV2D [64,28,28,128] x [128,3,3,128] (stride 1,
+pad 1) + per-channel DOUBLE_ROUND RESCALE to int8, with the distributions and
+zero points of the reference's int8 CONV2D+RESCALE configuration (x U[-128,127]
+zx=-3, w U zw=0, bias U[-2^15,2^15], multiplier U[2^30,2^31), shift U[30,40],
+output zp 5) at ResNet conv3_x scale, where int8 MFMA (not HBM) bounds it.
+
+The JSON line reports whole-job throughput (TOPS), the fused conv kernel's
+roofline (MFMA-bound; average duration from HIP events on the library's
+stream) and the CPU oracle timed on the host beside it; `extra` carries the
+other benchmark configurations (incl. the int8 MobileNetV2-style graph img/s).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA, 2.5 PFLOP/s
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
+METRIC = "int8 CONV2D+RESCALE TOPS (% MFMA peak); int8 MobileNetV2-style graph img/s"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--quick", action="store_true", help="headline workload only")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
+    return p.parse_args()
+
+
+class Runner:
+    """An Interpreter with device-resident inputs, running pipelined
+    (deferred) on torch's current stream."""
+
+    def __init__(self, T, torch, graph, inputs):
+        self.T, self.torch = T, torch
+        self.interp = T.Interpreter.from_flatbuffer(graph)
+        self.inputs = []
+        self.keep = []
+        for name, (arr, dt) in inputs.items():
+            dev = torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).reshape(-1).copy()).cuda()
+            self.keep.append(dev)
+            self.inputs.append(T.Tensor.from_device(name, arr.shape, dt, dev.data_ptr(), arr.nbytes, keep=dev))
+        torch.cuda.synchronize()
+
+    def run(self):
+        return self.interp.run(self.inputs)
+
+    def sync(self):
+        self.T.synchronize()
+        self.torch.cuda.synchronize()
+
+    def wall(self, steps, warmup):
+        for _ in range(warmup):
+            self.run()
+        self.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = self.run()
+        self.sync()
+        t1 = time.perf_counter()
+        del out
+        return (t1 - t0) / steps
+
+    def gpu_time(self, reps, sleep_cycles):
+        """Average GPU time of one run with host overhead hidden: the runs are
+        enqueued behind a spin kernel, so they execute back to back between
+        the two events."""
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(sleep_cycles)
+        e0.record()
+        outs = [self.run() for _ in range(reps)]
+        e1.record()
+        self.sync()
+        del outs
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def calibrate_sleep(torch, seconds):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cycles = 1_000_000
+    e0.record()
+    torch.cuda._sleep(cycles)
+    e1.record()
+    torch.cuda.synchronize()
+    per = max(e0.elapsed_time(e1) / 1e3, 1e-6) / cycles
+    return int(min(seconds / per, 2 ** 31 - 1))
+
+
+def cpu_baseline(seconds):
+    """The oracle (C restatement of the reference loops, 1 thread) on a
+    bounded sample of the headline workload: whole images of the batch until
+    `seconds` of CPU work; also checks the GPU's image-0 output bit for bit."""
+    from oracle import oracle as O
+    from tosa_amd import workloads as W
+    _, ins, info = W.conv_rescale(n=1, h=28, w=28, cin=128, cout=128)  # image 0 of the batch
+    x = ins["x"][0]
+    params = _conv_params()
+    done, t_total, out0 = 0, 0.0, None
+    xs = W.i8(W.rng(1, 0), (64, 28, 28, 128))
+    while t_total < seconds and done < 64:
+        xi = xs[done:done + 1]
+        t0 = time.perf_counter()
+        y = _oracle_conv_rescale(O, xi, params)
+        t_total += time.perf_counter() - t0
+        if done == 0:
+            out0 = y
+        done += 1
+    ops = done * info["ops"]
+    del x
+    return {"value": ops / t_total / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"{done} of 64 images of the headline CONV2D+RESCALE ({done * info['macs']:.3g} MAC) "
+                      f"through oracle/tosa_oracle.c (C restatement of the reference loops, 1 thread), "
+                      f"{t_total:.1f} s"}, out0
+
+
+def _conv_params():
+    from tosa_amd import workloads as W
+    cout, k, cin = 128, 3, 128
+    return {"w": W.i8(W.rng(1, 1), (cout, k, k, cin)),
+            "bias": W.rng(1, 2).integers(-2 ** 15, 2 ** 15 + 1, size=cout).astype(np.int32),
+            "mult": W.rng(1, 3).integers(2 ** 30, 2 ** 31, size=cout).astype(np.int64),
+            "shift": W.rng(1, 4).integers(30, 41, size=cout).astype(np.int8)}
+
+
+def _oracle_conv_rescale(O, x, p):
+    acc = O.conv2d(O.T("INT8", x.shape, x), O.T("INT8", p["w"].shape, p["w"]), O.T("INT32", p["bias"].shape, p["bias"]),
+                   -3, 0, [1, 1, 1, 1], [1, 1], [1, 1], "INT32", "INT32")
+    y = O.rescale(acc, O.T("INT32", [128], p["mult"]), O.T("INT8", [128], p["shift"]), 0, 5, "INT8", True, 3, True,
+                  False, False)
+    return y.vals.astype(np.int8).reshape(acc.shape)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path shards by batch with "
+              f"no exchange step, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import tosa_amd as T
+    from tosa_amd import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.init()
+    T.set_stream(torch.cuda.current_stream().cuda_stream)
+    T.set_option("deferred", 1)
+    sleep = calibrate_sleep(torch, 0.02)
+
+    # ---- headline: int8 CONV2D + RESCALE at ResNet conv3_x scale ----------
+    graph, ins, info = W.conv_rescale(n=64, h=28, w=28, cin=128, cout=128)
+    r = Runner(T, torch, graph, ins)
+    sec = r.wall(args.steps, args.warmup)
+    kern = r.gpu_time(20, sleep)
+    value = info["ops"] / sec / 1e12
+    achieved = info["ops"] / kern / 1e12
+    out_img0 = r.run()["y"].numpy()[0]
+    r.sync()
+
+    cpu, cpu_img0 = cpu_baseline(args.cpu_seconds)
+    extra = {"headline_image0_bit_exact_vs_oracle": bool(np.array_equal(out_img0, cpu_img0[0])),
+             "headline_kernel_us": kern * 1e6}
+
+    def measure(name, builder, unit_ops=True, steps=None, **kw):
+        g, i, inf = builder(**kw)
+        rr = Runner(T, torch, g, i)
+        s = rr.wall(steps or max(5, args.steps // 5), 2)
+        k = rr.gpu_time(5, sleep)
+        e = {"ms_per_step": s * 1e3, "gpu_ms": k * 1e3}
+        if unit_ops:
+            e["TOPS"] = inf["ops"] / k / 1e12
+        e["GB_s"] = inf["bytes"] / k / 1e9
+        extra[name] = e
+        return inf, s, k
+
+    if not args.quick:
+        inf, s, k = measure("mobilenet_v2_int8_n64", W.mobilenet_v2, n=64)
+        extra["mobilenet_v2_int8_n64"].update({"img_s": 64 / s, "img_s_gpu": 64 / k,
+                                               "hbm_roofline_frac": inf["bytes"] / k / 1e9 / PEAK_HBM_GBS})
+        measure("cfg1_conv_rescale_1x56x56x64", W.conv_rescale)
+        measure("conv_rescale_64x14x14x256", W.conv_rescale, n=64, h=14, w=14, cin=256, cout=256)
+        measure("cfg2_matmul_rescale_8x512x1024x1024", W.matmul_rescale)
+        measure("cfg3_depthwise_32x112x112x144_s2", W.depthwise)
+        measure("cfg3_avg_pool_32x7x7x1280", W.avg_pool, unit_ops=False)
+        measure("cfg5_bf16_conv3x3_64x28x28x128", W.float_conv, dtype="BF16")
+        measure("cfg5_fp16_conv3x3_64x28x28x128", W.float_conv, dtype="FP16")
+        measure("cfg5_bf16_conv1x1_64x28x28x128to512", W.float_conv, dtype="BF16", cout=512, k=1)
+        measure("cfg5_bf16_matmul_16x2048x2048x2048", W.float_matmul, steps=5)
+
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "int8 CONV2D [64,28,28,128]x[128,3,3,128] s1 p1 + per-channel DOUBLE_ROUND "
+                               "RESCALE->int8 (zx=-3, zw=0, output zp 5)",
+                   "global_batch": 64, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                     "frac": achieved / PEAK_INT8_TOPS, "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

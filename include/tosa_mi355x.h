@@ -163,12 +163,17 @@ tosa_status tosa_run_graph_with_hooks(const uint8_t* data, size_t len, tosa_tens
  * "fusion" (default 1): fold CONV2D/DEPTHWISE_CONV2D/MATMUL -> RESCALE ->
  * CLAMP chains and quantised residual adds into single kernels.
  * "strict_float" (default 0): run float CONV2D/MATMUL in the reference's
- * sequential order (bit-exact) instead of on MFMA. */
+ * sequential order (bit-exact) instead of on MFMA.
+ * "deferred" (default 0): tosa_run returns once its kernels are enqueued;
+ * value-dependent REQUIRE failures (RESCALE range/overflow) of such runs are
+ * reported by the next tosa_synchronize. Validation errors are unaffected. */
 tosa_status tosa_set_option(const char* key, int value);
 int tosa_get_option(const char* key);
 /* Run this thread's work on `hip_stream` (a hipStream_t); NULL restores the
  * library's own stream. */
 tosa_status tosa_set_stream(void* hip_stream);
+/* Waits for this thread's stream and reports REQUIRE failures of deferred
+ * runs (TOSA_ERR_GRAPH), clearing them. */
 tosa_status tosa_synchronize(void);
 int tosa_device_count(void);
 

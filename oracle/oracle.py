@@ -280,8 +280,9 @@ def _float_minmax(dtype, raw):
     return float(decode(dtype, v)[0])
 
 
-def run_block(block: fb.Block, inputs: dict) -> dict:
-    """Run `block` on `inputs` (name -> T) in the reference's ready-queue order."""
+def run_block(block: fb.Block, inputs: dict, order: list | None = None) -> dict:
+    """Run `block` on `inputs` (name -> T) in the reference's ready-queue order;
+    the executed operator indices are appended to `order` when given."""
     defs = {t.name: t for t in block.tensors}
     tensors = dict(inputs)
     ops = block.operators
@@ -297,6 +298,8 @@ def run_block(block: fb.Block, inputs: dict) -> dict:
         if done[i]:
             continue
         _eval(ops[i], tensors, defs)
+        if order is not None:
+            order.append(i)
         done[i] = True
         available.update(ops[i].outputs)
         for j, o in enumerate(ops):

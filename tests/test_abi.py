@@ -110,7 +110,8 @@ def test_error_if_cases_are_rejected_by_validation(d):
 def test_tensor_host_round_trip():
     for dt, arr in (("INT8", np.arange(-5, 5, dtype=np.int8)), ("INT48", np.array([-(2 ** 47), 2 ** 47 - 1])),
                     ("BF16", np.array([0x3F80, 0xC000], dtype=np.uint16)), ("FP32", np.linspace(0, 1, 7, dtype=np.float32)),
-                    ("INT32", np.zeros((0, 3), dtype=np.int32))):
+                    ("INT32", np.zeros((0, 3), dtype=np.int32)), ("BOOL", np.array(True)),
+                    ("INT8", np.int8(-3))):
         t = T.Tensor.from_numpy("t", arr, dt)
         assert t.dtype == dt and t.shape == list(arr.shape)
         assert np.array_equal(t.numpy(), arr.astype(t.numpy().dtype))

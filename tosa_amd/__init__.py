@@ -58,7 +58,9 @@ class Tensor:
         st = _np_storage(dtype)
         if dtype == "FP16" and a.dtype == np.float16:
             a = a.view(np.uint16)
-        a = np.ascontiguousarray(a.astype(st, copy=False)) if a.dtype != st else np.require(a, requirements="C")
+        a = a.astype(st, copy=False)
+        if not a.flags.c_contiguous:
+            a = a.copy(order="C")  # keeps rank 0, unlike np.ascontiguousarray
         shape = (ctypes.c_int64 * max(1, a.ndim))(*a.shape)
         h = ctypes.c_void_p()
         check(lib().tosa_tensor_from_host(name.encode(), shape, a.ndim, DTYPE_CODE[dtype],

@@ -555,6 +555,8 @@ tosa_status tosa_set_option(const char* key, int value)
         o.fusion = value != 0;
     else if (std::strcmp(key, "strict_float") == 0)
         o.strict_float = value != 0;
+    else if (std::strcmp(key, "deferred") == 0)
+        o.deferred = value != 0;
     else
         return fail(TOSA_ERR_INVALID_ARGUMENT, std::string("unknown option ") + key);
     return TOSA_OK;
@@ -569,6 +571,8 @@ int tosa_get_option(const char* key)
         return o.fusion;
     if (std::strcmp(key, "strict_float") == 0)
         return o.strict_float;
+    if (std::strcmp(key, "deferred") == 0)
+        return o.deferred;
     return -1;
 }
 
@@ -580,7 +584,14 @@ tosa_status tosa_set_stream(void* hip_stream)
 
 tosa_status tosa_synchronize(void)
 {
-    return guard([] { hip_check(hipStreamSynchronize(thread_stream().s), "hipStreamSynchronize"); });
+    return guard([] {
+        Stream& s = thread_stream();
+        const uint32_t e = read_error_word(s);  // synchronises the stream
+        if (e) {
+            clear_error_word(s);
+            throw Error(ERR_GRAPH, device_error_message(e));
+        }
+    });
 }
 
 int tosa_device_count(void) { return device_count(); }

@@ -19,6 +19,10 @@ namespace tosa {
 struct RunOptions {
     bool fusion = true;         // fold RESCALE/CLAMP/residual chains into one kernel
     bool strict_float = false;  // float CONV2D/MATMUL in the reference's sequential order
+    // Pipelined runs: run() returns once its kernels are enqueued, without
+    // synchronising or reading the error word; REQUIRE failures of any
+    // deferred run are reported by the next synchronize().
+    bool deferred = false;
 };
 
 // CONST payloads decoded once per graph. Their storages become
@@ -74,7 +78,8 @@ public:
     {
         if (!stream_) {
             stream_ = &thread_stream();
-            clear_error_word(*stream_);
+            if (!opts.deferred)
+                clear_error_word(*stream_);
         }
         return *stream_;
     }

@@ -29,6 +29,8 @@ RunOptions& default_run_options()
             o.fusion = std::atoi(f) != 0;
         if (const char* s = std::getenv("TOSA_MI355X_STRICT_FLOAT"))
             o.strict_float = std::atoi(s) != 0;
+        if (const char* d = std::getenv("TOSA_MI355X_DEFERRED"))
+            o.deferred = std::atoi(d) != 0;
         return o;
     }();
     return opts;
@@ -266,7 +268,7 @@ TensorMap Interpreter::run(const TensorMap& inputs, InterpreterHook& hook, const
         }
         outputs.emplace(name, t);
     }
-    if (st.has_stream()) {
+    if (st.has_stream() && !st.opts.deferred) {
         if (uint32_t e = read_error_word(st.stream()))
             throw Error(ERR_GRAPH, device_error_message(e));
     }
