@@ -79,13 +79,14 @@ class Runner:
     def gpu_time(self, reps, sleep_cycles):
         """Average GPU time of one run with host overhead hidden: the runs are
         enqueued behind a spin kernel, so they execute back to back between
-        the two events."""
+        the two events, all on the stream the library launches on."""
         torch = self.torch
+        s = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda._sleep(sleep_cycles)
-        e0.record()
+        e0.record(s)
         outs = [self.run() for _ in range(reps)]
-        e1.record()
+        e1.record(s)
         self.sync()
         del outs
         return e0.elapsed_time(e1) / 1e3 / reps
@@ -94,9 +95,10 @@ class Runner:
 def calibrate_sleep(torch, seconds):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     cycles = 1_000_000
-    e0.record()
+    s = torch.cuda.current_stream()
+    e0.record(s)
     torch.cuda._sleep(cycles)
-    e1.record()
+    e1.record(s)
     torch.cuda.synchronize()
     per = max(e0.elapsed_time(e1) / 1e3, 1e-6) / cycles
     return int(min(seconds / per, 2 ** 31 - 1))
@@ -160,7 +162,12 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.init()
-    T.set_stream(torch.cuda.current_stream().cuda_stream)
+    # A stream of our own (default priority): the library launches on it and
+    # the timing events are recorded on it. (torch's default stream is the
+    # NULL stream, which set_stream would read as "library-owned stream".)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    T.set_stream(stream.cuda_stream)
     T.set_option("deferred", 1)
     sleep = calibrate_sleep(torch, 0.02)
 

@@ -132,10 +132,29 @@ def loaded() -> bool:
     return _LIB is not None
 
 
+def _bind_process_hip_runtime():
+    """Make this process use one HIP runtime. PyTorch-ROCm ships its own
+    libamdhip64 (soname libamdhip64.so.7, but loaded by torch as
+    "libamdhip64.so" from its own directory); if ours were loaded first, a
+    later `import torch` would bring in a second runtime and the two would
+    contend for the device. Loading torch's copy first, globally, makes this
+    library bind to it too (same soname), and torch then reuses the same file."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    for d in spec.submodule_search_locations:
+        hip = os.path.join(d, "lib", "libamdhip64.so")
+        if os.path.exists(hip):
+            ctypes.CDLL(hip, mode=ctypes.RTLD_GLOBAL)
+            return
+
+
 def lib():
     """The loaded library. Raises if it was not built: there is no fallback."""
     global _LIB
     if _LIB is None:
+        _bind_process_hip_runtime()
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `python -m tosa_amd.build` "
