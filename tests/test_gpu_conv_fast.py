@@ -1,0 +1,190 @@
+"""GPU parity of the int8 MFMA convolution with the table-driven epilogue
+(tosa_amd/csrc/kernels/conv_i8.hip) against the oracle, bit for bit.
+
+The sweep covers the kernel's template variants: tap-uniform stages of 64 and
+128 bytes (IC a multiple of 64 / 128) and 1x1 stride-1 convolutions over any
+IC that is a multiple of 16; channel tiles of 16/32/64/128 with ragged output
+channel counts; pixel counts that are not a multiple of the tile; nonzero
+input and weight zero points; int32, and RESCALE to int8/int16/int32 with
+per-channel and per-tensor SINGLE/DOUBLE rounding, shifts below 32 (where
+apply_scale_32's value-range REQUIRE is live), output zero points, a fused
+CLAMP, and biases near +-2^31 so the accumulator wraps.
+"""
+
+import numpy as np
+import pytest
+
+import tosa_amd as T
+from oracle import oracle as O
+from oracle import tosa_reader as fb
+from tosa_amd.tosa_writer import GraphBuilder
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_run(graph, ins):
+    blk = fb.main_block(graph)
+    return O.run_block(blk, {n: O.T(dt, list(a.shape), O.decode(dt, a)) for n, (a, dt) in ins.items()})
+
+
+def run(graph, ins, fusion=True):
+    old = T.get_option("fusion")
+    T.set_option("fusion", int(fusion))
+    try:
+        return T.run_graph(graph, [T.Tensor.from_numpy(n, a, dt) for n, (a, dt) in ins.items()])
+    finally:
+        T.set_option("fusion", old)
+
+
+def build(x, w, bias, zx, zw, pad, stride, dil, rescale=None, out_dtype="INT8", clamp=None, bias_input=False):
+    n, ih, iw, _ = x.shape
+    oc, kh, kw, _ = w.shape
+    oh = (ih - 1 + pad[0] + pad[1] - (kh - 1) * dil[0]) // stride[0] + 1
+    ow = (iw - 1 + pad[2] + pad[3] - (kw - 1) * dil[1]) // stride[1] + 1
+    g = GraphBuilder()
+    g.input("x", x.shape, "INT8")
+    g.const("w", w, "INT8")
+    if bias_input:
+        g.input("b", bias.shape, "INT32")
+    else:
+        g.const("b", bias, "INT32")
+    g.const("zx", np.array([zx]), "INT8")
+    g.const("zw", np.array([zw]), "INT8")
+    g.tensor("acc", [n, oh, ow, oc], "INT32")
+    g.op("CONV2D", ["x", "w", "b", "zx", "zw"], ["acc"], pad=list(pad), stride=list(stride), dilation=list(dil),
+         acc_type="INT32")
+    out = "acc"
+    if rescale is not None:
+        mult, shift, ozp, dbl, pc = rescale
+        g.const("m", np.asarray(mult, np.int32), "INT32")
+        g.const("s", np.asarray(shift, np.int8), "INT8")
+        g.const("iz", np.array([0]), "INT32")
+        g.const("oz", np.array([ozp]), out_dtype)
+        g.tensor("q", [n, oh, ow, oc], out_dtype)
+        g.op("RESCALE", ["acc", "m", "s", "iz", "oz"], ["q"], scale32=1,
+             rounding_mode="DOUBLE_ROUND" if dbl else "SINGLE_ROUND", per_channel=int(pc))
+        out = "q"
+        if clamp is not None:
+            g.tensor("c", [n, oh, ow, oc], out_dtype)
+            width = {"INT8": 1, "INT16": 2, "INT32": 4}[out_dtype]
+            lo = int(clamp[0]).to_bytes(width, "little", signed=True) + bytes(8 - width)
+            hi = int(clamp[1]).to_bytes(width, "little", signed=True) + bytes(8 - width)
+            g.op("CLAMP", ["q"], ["c"], min_val=lo, max_val=hi)
+            out = "c"
+    return g.build([out]), out
+
+
+def check(graph, out, ins):
+    ref = oracle_run(graph, ins)[out]
+    for fusion in (True, False):
+        got = run(graph, ins, fusion)[out].numpy()
+        assert np.array_equal(got.reshape(-1).astype(np.int64), ref.vals.reshape(-1).astype(np.int64)), fusion
+
+
+TAPS = [(3, 3, 64), (3, 3, 128), (5, 5, 64), (1, 3, 192), (3, 1, 256), (3, 3, 256), (2, 2, 128), (1, 1, 64)]
+OCS = [8, 16, 24, 40, 64, 96, 128, 130, 200, 256]
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_fast_conv_taps(seed):
+    rng = np.random.default_rng(5000 + seed)
+    kh, kw, ic = TAPS[seed % len(TAPS)]
+    oc = OCS[(seed * 3) % len(OCS)]
+    n, ih, iw = int(rng.integers(1, 3)), int(rng.integers(5, 15)), int(rng.integers(5, 15))
+    stride = [int(rng.integers(1, 3)), int(rng.integers(1, 3))]
+    dil = [int(rng.integers(1, 3)), 1]
+    pad = [int(v) for v in rng.integers(0, 3, size=4)]
+    for d, (i, k) in enumerate(((ih, kh), (iw, kw))):
+        full = i - 1 + pad[2 * d] + pad[2 * d + 1] - (k - 1) * dil[d]
+        if full < 0:
+            pad[2 * d + 1] += -full
+            full = 0
+        pad[2 * d + 1] += (-full) % stride[d]
+    x = rng.integers(-128, 128, size=(n, ih, iw, ic)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(oc, kh, kw, ic)).astype(np.int8)
+    bias = (rng.integers(2 ** 31 - 2 ** 20, 2 ** 31, size=oc) * rng.choice([-1, 1], size=oc)).astype(np.int32)
+    zx = int(rng.integers(-128, 128))
+    zw = int(rng.integers(-128, 128)) if seed % 3 else 0
+    mode = seed % 4
+    if mode == 0:
+        graph, out = build(x, w, bias, zx, zw, pad, stride, dil)
+    else:
+        out_dtype = ["INT8", "INT16", "INT32"][seed % 3]
+        ozp = int(rng.integers(-128, 128)) if out_dtype == "INT8" else 0
+        pc = mode != 3
+        cnt = oc if pc else 1
+        rs = (rng.integers(0, 2 ** 31, size=cnt), rng.integers(40, 56, size=cnt), ozp, bool(mode == 1), pc)
+        # CLAMP takes int8 and int16 only (src/ops/elementwise.rs:327).
+        clamp = (-20, 100) if seed % 5 == 0 and out_dtype != "INT32" else None
+        graph, out = build(x, w, bias, zx, zw, pad, stride, dil, rescale=rs, out_dtype=out_dtype, clamp=clamp)
+    check(graph, out, {"x": (x, "INT8")})
+
+
+PW_IC = [16, 32, 48, 96, 144, 160, 64, 320]
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_fast_conv_pointwise(seed):
+    rng = np.random.default_rng(6000 + seed)
+    ic = PW_IC[seed % len(PW_IC)]
+    oc = OCS[(seed * 7) % len(OCS)]
+    n, h, w_ = int(rng.integers(1, 4)), int(rng.integers(3, 20)), int(rng.integers(3, 20))
+    x = rng.integers(-128, 128, size=(n, h, w_, ic)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(oc, 1, 1, ic)).astype(np.int8)
+    bias = rng.integers(-2 ** 31, 2 ** 31, size=oc).astype(np.int32)
+    zx = int(rng.integers(-128, 128))
+    zw = int(rng.integers(-5, 6)) if seed % 2 else 0
+    dbl = bool(seed % 2)
+    # Shifts from 20 upwards: below 32 the value-range REQUIRE is live, so the
+    # accumulators are kept small (weights in [-2, 2]) for those seeds.
+    if seed % 4 == 3:
+        w = rng.integers(-2, 3, size=(oc, 1, 1, ic)).astype(np.int8)
+        bias = rng.integers(-1000, 1000, size=oc).astype(np.int32)
+        shift = rng.integers(24, 32, size=oc)
+    else:
+        shift = rng.integers(36, 50, size=oc)
+    rs = (rng.integers(2 ** 30, 2 ** 31, size=oc), shift, int(rng.integers(-16, 17)), dbl, True)
+    clamp = (int(rng.integers(-128, 0)), 127) if seed % 3 == 0 else None
+    graph, out = build(x, w, bias, zx, zw, [0, 0, 0, 0], [1, 1], [1, 1], rescale=rs, clamp=clamp)
+    check(graph, out, {"x": (x, "INT8")})
+
+
+def test_fast_conv_table_cache_and_runtime_bias():
+    """The same interpreter run twice (the second run uses the cached
+    epilogue table), and a bias that is a graph input (never cached)."""
+    rng = np.random.default_rng(77)
+    x = rng.integers(-128, 128, size=(2, 9, 9, 128)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(64, 3, 3, 128)).astype(np.int8)
+    bias = rng.integers(-2 ** 20, 2 ** 20, size=64).astype(np.int32)
+    rs = (rng.integers(2 ** 30, 2 ** 31, size=64), rng.integers(30, 40, size=64), 5, True, True)
+    graph, out = build(x, w, bias, -3, 0, [1, 1, 1, 1], [1, 1], [1, 1], rescale=rs)
+    ins = {"x": (x, "INT8")}
+    ref = oracle_run(graph, ins)[out].vals
+    interp = T.Interpreter.from_flatbuffer(graph)
+    for _ in range(3):
+        got = interp.run([T.Tensor.from_numpy("x", x, "INT8")])[out].numpy()
+        assert np.array_equal(got.reshape(-1).astype(np.int64), ref.astype(np.int64))
+
+    graph2, out2 = build(x, w, bias, -3, 0, [1, 1, 1, 1], [1, 1], [1, 1], rescale=rs, bias_input=True)
+    interp2 = T.Interpreter.from_flatbuffer(graph2)
+    for b in (bias, bias + 12345):
+        ins2 = {"x": (x, "INT8"), "b": (b.astype(np.int32), "INT32")}
+        ref2 = oracle_run(graph2, ins2)[out2].vals
+        got = interp2.run([T.Tensor.from_numpy(k, a, dt) for k, (a, dt) in ins2.items()])[out2].numpy()
+        assert np.array_equal(got.reshape(-1).astype(np.int64), ref2.astype(np.int64))
+
+
+def test_fast_conv_require_failure():
+    """A shift below 32 with accumulators outside [-2^(s-1), 2^(s-1)) is
+    apply_scale_32's REQUIRE failure: the run reports GraphError."""
+    rng = np.random.default_rng(78)
+    x = rng.integers(-128, 128, size=(1, 8, 8, 64)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(32, 3, 3, 64)).astype(np.int8)
+    bias = np.zeros(32, np.int32)
+    rs = (np.full(32, 2 ** 30), np.full(32, 8), 0, False, True)
+    graph, out = build(x, w, bias, 0, 0, [1, 1, 1, 1], [1, 1], [1, 1], rescale=rs)
+    with pytest.raises(T.TosaError) as e:
+        run(graph, {"x": (x, "INT8")})
+    assert e.value.kind == "GraphError"
+    with pytest.raises(O.OracleError):
+        oracle_run(graph, {"x": (x, "INT8")})

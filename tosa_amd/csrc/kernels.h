@@ -77,6 +77,35 @@ void gemm(const GemmDesc& d, const void* x, const void* w, void* out, uint32_t* 
 void weight_sums_i8(const int8_t* w, int32_t oc, int32_t k, int32_t* wsum, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
+// int8 CONV2D on MFMA with a table-driven epilogue (conv_i8.hip)
+// ---------------------------------------------------------------------------
+struct ConvI8Desc {
+    const int8_t* x = nullptr;     // NHWC [n, ih, iw, ic]
+    const int8_t* w = nullptr;     // OHWI [oc, kh, kw, ic]
+    const int32_t* bias = nullptr; // [bias_len], bias_len 1 or oc
+    int32_t bias_len = 1;
+    int32_t n = 1, ih = 1, iw = 1, ic = 1, oc = 1, kh = 1, kw = 1, oh = 1, ow = 1;
+    int32_t pt = 0, pl = 0, sy = 1, sx = 1, dy = 1, dx = 1;
+    int32_t zp_x = 0, zp_w = 0;
+};
+// Geometry and alignment the kernel handles: 1x1 stride-1 unpadded
+// convolutions with ic % 16 == 0, any other geometry with ic % 64 == 0;
+// 16-byte aligned x and w.
+bool conv_i8_fast_supported(const ConvI8Desc& d);
+// RESCALEs the fused epilogue handles: scale32 with SINGLE or DOUBLE
+// rounding, signed input with zero point 0 (the only legal one for int32).
+bool conv_i8_fast_epilogue_ok(const RescaleDev& rs);
+// Per-channel epilogue table (8 int32 per output channel) built on the
+// device from w, bias, the zero points and, when `rs` is given, the RESCALE
+// multiplier and shift.
+constexpr int CONV_I8_TABLE_WORDS = 8;
+void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStream_t stream);
+// The convolution; `rs` selects the fused RESCALE (+CLAMP) epilogue with the
+// table built for the same `rs`, else the int32 output (conv + bias).
+void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                  hipStream_t stream);
+
+// ---------------------------------------------------------------------------
 // Reference-order kernels (one thread per output, the reference's loop
 // order and rounding, so float results are bit-identical to a sequential
 // evaluation). They cover every type combination the MFMA path does not.

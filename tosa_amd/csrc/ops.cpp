@@ -5,7 +5,9 @@
 // unsupported.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <optional>
 
 #include "exec.h"
@@ -207,6 +209,42 @@ StoragePtr cached_aux(Storage& owner, int kind, const std::function<StoragePtr()
 }
 
 enum AuxKind { AUX_WSUM = 1, AUX_F32 = 2, AUX_RESCALE = 3 };
+
+std::mutex& derived_mu()
+{
+    static std::mutex mu;
+    return mu;
+}
+
+// Epilogue table of the fast int8 convolution for `rs` (the plain int32
+// epilogue when null). Cached on the weight storage when everything it is
+// built from is a graph constant (`cacheable`); the table kernel then
+// completes before the table is shared, so runs on other streams see it.
+StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* bias_key, const RescaleDev* rs,
+                             bool cacheable, hipStream_t s)
+{
+    std::string key;
+    if (cacheable) {
+        char buf[192];
+        std::snprintf(buf, sizeof buf, "conv_i8_tab:%p:%d:%d:%d:%p:%p:%d:%d", bias_key, d.bias_len, d.zp_x, d.zp_w,
+                      rs ? static_cast<const void*>(rs->mult) : nullptr,
+                      rs ? static_cast<const void*>(rs->shift) : nullptr, rs ? rs->per_channel : 0,
+                      rs ? rs->rounding : 0);
+        key = buf;
+        std::lock_guard<std::mutex> lk(derived_mu());
+        auto it = wstore.derived.find(key);
+        if (it != wstore.derived.end())
+            return it->second;
+    }
+    auto t = make_device_storage(DT_INT32, int64_t(CONV_I8_TABLE_WORDS) * d.oc);
+    conv_i8_table(d, rs, t->device_out(), s);
+    if (cacheable) {
+        hip_check(hipStreamSynchronize(s), "conv_i8 table");
+        std::lock_guard<std::mutex> lk(derived_mu());
+        wstore.derived[key] = t;
+    }
+    return t;
+}
 
 // ---------------------------------------------------------------------------
 // RESCALE preparation: every check of eval_rescale (src/ops/type_conv.rs:
@@ -696,17 +734,50 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
     };
 
     if ((mfma_int || dw_int) && sizes_ok()) {
-        // Per-channel weight sums, needed when the input zero point is not 0.
+        const void* x = input->data->device_in();
+        const void* w = weight->data->device_in();
+        // Weight and bias are graph constants: derived data may be cached.
+        const bool wb_const = st.const_defs.count(op.inputs[1]) && st.const_defs.count(op.inputs[2]);
+        ConvI8Desc fd;
+        bool fast = false;
+        if (mfma_int) {
+            fd.x = static_cast<const int8_t*>(x);
+            fd.w = static_cast<const int8_t*>(w);
+            fd.bias = static_cast<const int32_t*>(bias->data->device_in());
+            fd.bias_len = int32_t(bc);
+            fd.n = int32_t(g.n);
+            fd.ih = int32_t(g.ih);
+            fd.iw = int32_t(g.iw);
+            fd.ic = int32_t(g.ic);
+            fd.oc = int32_t(g.oc);
+            fd.kh = int32_t(g.kh);
+            fd.kw = int32_t(g.kw);
+            fd.oh = int32_t(g.oh);
+            fd.ow = int32_t(g.ow);
+            fd.pt = int32_t(g.pt);
+            fd.pl = int32_t(g.pl);
+            fd.sy = int32_t(g.sy);
+            fd.sx = int32_t(g.sx);
+            fd.dy = int32_t(g.dy);
+            fd.dx = int32_t(g.dx);
+            fd.zp_x = int32_t(izp);
+            fd.zp_w = int32_t(wzp);
+            fast = conv_i8_fast_supported(fd);
+        }
+        // Per-channel weight sums for the generic kernel, needed when the
+        // input zero point is not 0.
         const int32_t* wsum = nullptr;
+        StoragePtr wsum_keep;
         if (izp != 0 && mfma_int) {
             Storage& ws = *weight->data;
-            auto sums = cached_aux(ws, AUX_WSUM, [&]() {
+            auto make = [&]() {
                 auto s = make_device_storage(DT_INT32, g.oc);
                 weight_sums_i8(static_cast<const int8_t*>(ws.device_in()), int32_t(g.oc), int32_t(K),
                                static_cast<int32_t*>(s->device_out()), st.s());
                 return s;
-            });
-            wsum = static_cast<const int32_t*>(sums->device_in());
+            };
+            wsum_keep = st.const_defs.count(op.inputs[1]) ? cached_aux(ws, AUX_WSUM, make) : make();
+            wsum = static_cast<const int32_t*>(wsum_keep->device_in());
         }
         GemmDesc gd;
         DepthwiseDesc dd{};
@@ -753,12 +824,15 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             dd.bias = static_cast<const int32_t*>(bias->data->device_in());
             dd.bias_len = int32_t(bc);
         }
-        const void* x = input->data->device_in();
-        const void* w = weight->data->device_in();
         // Keep the operands alive for a later recomputation of a fused-away
         // int32 output.
-        auto launch = [gd, dd, mfma_int, x, w, input, weight, bias](void* out, const RescaleDev* rs, uint32_t* err,
-                                                                      hipStream_t s) {
+        auto launch = [gd, dd, mfma_int, fast, fd, wb_const, x, w, input, weight, bias, wsum_keep](
+                          void* out, const RescaleDev* rs, bool rs_const, uint32_t* err, hipStream_t s) {
+            if (fast && (!rs || conv_i8_fast_epilogue_ok(*rs))) {
+                auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), rs, wb_const && (!rs || rs_const), s);
+                conv_i8_fast(fd, tab->device_in(), rs, out, err, s);
+                return;
+            }
             if (mfma_int) {
                 GemmDesc d = gd;
                 if (rs) {
@@ -778,13 +852,15 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         if (auto tail = plan_tail(st, index, g.out_shape)) {
             const DType final_t = tail->rp.out_t;
             auto fin = new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], g.out_shape, final_t);
+            const bool rs_const =
+                st.const_defs.count(tail->rop->inputs[1]) && st.const_defs.count(tail->rop->inputs[2]);
             if (count > 0)
-                launch(fin->data->device_out(), &tail->rp.rs, st.err(), st.s());
+                launch(fin->data->device_out(), &tail->rp.rs, rs_const, st.err(), st.s());
             auto keep = tail->rp.params;
             finish_fused(st, out_name, g.out_shape, *tail, fin, [launch, keep](Storage& o) {
                 Stream& s = thread_stream();
                 if (o.count > 0)
-                    launch(o.device_out(), nullptr, s.err, s.s);
+                    launch(o.device_out(), nullptr, false, s.err, s.s);
                 else
                     o.device_out();
             });
@@ -793,7 +869,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         auto out = new_output(out_name, g.out_shape, DT_INT32);
         void* od = out->data->device_out();
         if (count > 0)
-            launch(od, nullptr, st.err(), st.s());
+            launch(od, nullptr, false, st.err(), st.s());
         st.set(out);
         return;
     }

@@ -20,6 +20,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <functional>
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -48,6 +49,10 @@ struct Storage {
     // sums of a convolution weight); valid as long as this storage is.
     std::shared_ptr<Storage> aux;
     int aux_kind = 0;
+    // Further derived data keyed by what it was built from (e.g. the
+    // epilogue table of a convolution for one bias / RESCALE combination).
+    // Only immutable (graph constant) sources may be cached here.
+    std::map<std::string, std::shared_ptr<Storage>> derived;
 
     Storage() = default;
     Storage(const Storage&) = delete;
