@@ -46,8 +46,8 @@ struct ConvI8Args {
     int32_t ih, iw, kw, ohow, ow, pt, pl, sy, sx, dy, dx;
     FastDiv div_ohow, div_ow;
     int32_t zp_x, zp_w;
-    int32_t out_zp;    // RESCALE output zero point
-    int32_t zp_limit;  // r + out_zp leaves int32 when r > zp_limit (out_zp > 0) or r < zp_limit (out_zp < 0)
+    int32_t out_zp;          // RESCALE output zero point
+    int32_t zp_lo, zp_hi;    // r + out_zp stays in int32 iff zp_lo <= r <= zp_hi
     int32_t lo, hi;    // output type range
     int32_t clo, chi;  // CLAMP bounds (the output range when there is no CLAMP)
     uint32_t* err;
@@ -116,13 +116,13 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
             pix[p] = ox * A.sx - A.pl;
         }
     }
+    // Weight rows past N re-read row N-1: their products land in output
+    // channels that are never stored.
     int32_t wbase[QCH];
-    bool wok[QCH];
 #pragma unroll
     for (int q = 0; q < QCH; q++) {
-        const int row = r0 + RPP * q;
-        wok[q] = row < BC && n0 + row < A.N;
-        wbase[q] = (n0 + row) * A.K;
+        const int oc = n0 + r0 + RPP * q;
+        wbase[q] = (oc < A.N ? oc : A.N - 1) * A.K;
     }
 
     const uint32_t zf = uint32_t(uint8_t(A.zp_x)) * 0x01010101u;
@@ -161,13 +161,12 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
                 rsum[p] = s;
             }
         }
+        // Chunks past K (pointwise K not a multiple of KC) re-read the row's
+        // last 16 bytes; the pixel side is zero there, so they add nothing.
+        const int kw_off = kc < A.K ? kc : A.K - 16;
 #pragma unroll
         for (int q = 0; q < QCH; q++)
-        {
-            const bool ok = wok[q] && kc < A.K;
-            const v4u v = ld16(A.w + (ok ? wbase[q] + kc : 0));
-            qr[q] = ok ? v : zero;
-        }
+            qr[q] = ld16(A.w + wbase[q] + kw_off);
     };
     auto store = [&](int buf) {
 #pragma unroll
@@ -178,10 +177,17 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
 #pragma unroll
         for (int q = 0; q < QCH; q++) {
             const int row = r0 + RPP * q;
-            if (row < BC)
+            if (BC % RPP == 0 || row < BC)
                 *reinterpret_cast<v4u*>(sA + buf * BC * KC + row * KC + ((ch ^ swz<KC>(row)) << 4)) = qr[q];
         }
     };
+
+    // The tile's epilogue table, staged in LDS behind the stage buffers.
+    v4i* const s_tab = reinterpret_cast<v4i*>(smem + 2 * (BC + BP) * KC);
+    for (int i = tid; i < 2 * BC; i += 256) {
+        const int c = n0 + (i >> 1);
+        s_tab[i] = A.tab[2 * (c < A.N ? c : A.N - 1) + (i & 1)];
+    }
 
     v4i acc[TM][TN];
 #pragma unroll
@@ -260,21 +266,25 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
     }
 
     // ---- epilogue ----------------------------------------------------------
-    const int c0 = n0 + wave_c0 + grp * 4 * TM;  // first channel held by this lane
-    bool bad_range = false, bad_result = false, bad_zp = false;
+    const int cl0 = wave_c0 + grp * 4 * TM;  // first tile channel held by this lane
+    const int c0 = n0 + cl0;
+    bool bad_range = false, bad_zp = false;
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
+        // One channel group at a time: keeps the scheduler from hoisting every
+        // group's table reads (32 registers each) to the top.
+        __builtin_amdgcn_sched_barrier(0);
         v4i t0[4], t1[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int c = c0 + 4 * tm + i;
-            const int cc = c < A.N ? c : A.N - 1;
-            t0[i] = A.tab[2 * cc];
+            t0[i] = s_tab[2 * (cl0 + 4 * tm + i)];
             if constexpr (RS)
-                t1[i] = A.tab[2 * cc + 1];
+                t1[i] = s_tab[2 * (cl0 + 4 * tm + i) + 1];
         }
 #pragma unroll
         for (int tn = 0; tn < TN; tn++) {
+            // Four outputs at a time (bounds the 64-bit temporaries in flight).
+            __builtin_amdgcn_sched_barrier(0);
             int32_t zwx = 0;
             if constexpr (ZW)
                 zwx = int32_t(uint32_t(A.zp_w) * uint32_t(s_rowsum[wave_p0 + 16 * tn + j16]));
@@ -289,16 +299,19 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
                     bad_range |= uint32_t(hi_bits + 1) > 1u;
                     const int64_t rnd = x >= 0 ? ((int64_t(t1[i].y) << 32) | uint32_t(t1[i].x))
                                                : ((int64_t(t1[i].w) << 32) | uint32_t(t1[i].z));
+                    // With the value in range and 0 <= multiplier < 2^31 the
+                    // scaled result always fits int32 (|r| <= 2^30 + 1), so
+                    // apply_scale_32's result REQUIRE cannot fail here.
                     const int64_t r = (int64_t(x) * int64_t(t0[i].y) + rnd) >> t0[i].w;
                     const int32_t r32 = int32_t(r);
-                    bad_result |= int32_t(r >> 32) != (r32 >> 31);
-                    if (A.out_zp > 0)
-                        bad_zp |= r32 > A.zp_limit;
-                    else if (A.out_zp < 0)
-                        bad_zp |= r32 < A.zp_limit;
+                    bad_zp |= (r32 < A.zp_lo) | (r32 > A.zp_hi);
                     int32_t v = r32 + A.out_zp;
                     v = v < A.lo ? A.lo : (v > A.hi ? A.hi : v);
                     v = v < A.clo ? A.clo : (v > A.chi ? A.chi : v);
+                    // Materialise the 32-bit result here: otherwise the
+                    // 64-bit intermediates are sunk towards the final stores
+                    // and held in registers across every group.
+                    asm volatile("" : "+v"(v));
                     acc[tm][tn][i] = v;
                 } else {
                     acc[tm][tn][i] = x;
@@ -358,8 +371,6 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
     }
     if (bad_range)
         atomicOr(A.err, DERR_SCALE_RANGE);
-    if (bad_result)
-        atomicOr(A.err, DERR_SCALE_RESULT);
     if (bad_zp)
         atomicOr(A.err, DERR_RESCALE_I32);
 }
@@ -405,7 +416,7 @@ template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool
 void launch(const ConvI8Args& a, hipStream_t s)
 {
     auto kfn = conv_i8_kernel<BC, BP, WC, WP, KC, PW, OB, RS, ZW>;
-    constexpr size_t lds = size_t(2) * (BC + BP) * KC;
+    constexpr size_t lds = size_t(2) * (BC + BP) * KC + size_t(32) * BC;
     static_assert(lds >= 4 * BP, "rowsum scratch");
     static bool attr = [&]() {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -517,7 +528,8 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     int ob = 4;
     if (rs) {
         a.out_zp = int32_t(rs->out_zp);
-        a.zp_limit = rs->out_zp > 0 ? int32_t(INT32_MAX - rs->out_zp) : int32_t(INT32_MIN - rs->out_zp);
+        a.zp_lo = rs->out_zp < 0 ? int32_t(INT32_MIN - rs->out_zp) : INT32_MIN;
+        a.zp_hi = rs->out_zp > 0 ? int32_t(INT32_MAX - rs->out_zp) : INT32_MAX;
         a.lo = int32_t(rs->lo);
         a.hi = int32_t(rs->hi);
         a.clo = rs->has_clamp ? int32_t(rs->clamp_lo) : a.lo;
