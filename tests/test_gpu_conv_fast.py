@@ -188,3 +188,43 @@ def test_fast_conv_require_failure():
     assert e.value.kind == "GraphError"
     with pytest.raises(O.OracleError):
         oracle_run(graph, {"x": (x, "INT8")})
+
+
+# Stride-1 shapes that take the halo-tiled kernel: output rows of 14..56
+# pixels so a workgroup tile holds >= 112 pixels; IC 512 with a 28-wide image
+# needs two halo passes of 256 channels.
+HALO = [
+    # n, h, w, ic, oc, kh, kw, dil, pad
+    (2, 28, 28, 128, 128, 3, 3, (1, 1), (1, 1, 1, 1)),
+    (1, 14, 14, 256, 256, 3, 3, (1, 1), (1, 1, 1, 1)),
+    (1, 30, 20, 64, 40, 5, 5, (1, 1), (2, 2, 2, 2)),
+    (2, 17, 23, 192, 130, 1, 3, (1, 1), (0, 0, 1, 1)),
+    (1, 23, 17, 128, 64, 3, 1, (2, 1), (2, 2, 0, 0)),
+    (1, 28, 28, 512, 96, 3, 3, (1, 1), (1, 1, 1, 1)),
+    (1, 29, 31, 64, 200, 2, 2, (1, 2), (0, 1, 1, 0)),
+    (3, 16, 16, 320, 24, 3, 3, (2, 2), (2, 2, 2, 2)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(HALO)))
+@pytest.mark.parametrize("mode", ["i32", "rescale_i8", "rescale_i16_zw"])
+def test_fast_conv_halo(case, mode):
+    n, h, w_, ic, oc, kh, kw, dil, pad = HALO[case]
+    rng = np.random.default_rng(7000 + 10 * case + len(mode))
+    oh = h - 1 + pad[0] + pad[1] - (kh - 1) * dil[0] + 1
+    ow = w_ - 1 + pad[2] + pad[3] - (kw - 1) * dil[1] + 1
+    assert oh > 0 and ow > 0
+    x = rng.integers(-128, 128, size=(n, h, w_, ic)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(oc, kh, kw, ic)).astype(np.int8)
+    bias = (rng.integers(2 ** 31 - 2 ** 20, 2 ** 31, size=oc) * rng.choice([-1, 1], size=oc)).astype(np.int32)
+    zx = int(rng.integers(-128, 128))
+    zw = int(rng.integers(-128, 128)) if mode.endswith("zw") else 0
+    if mode == "i32":
+        graph, out = build(x, w, bias, zx, zw, pad, [1, 1], list(dil))
+    else:
+        out_dtype = "INT16" if "i16" in mode else "INT8"
+        ozp = 0 if out_dtype == "INT16" else int(rng.integers(-128, 128))
+        rs = (rng.integers(2 ** 30, 2 ** 31, size=oc), rng.integers(38, 50, size=oc), ozp, case % 2 == 0, True)
+        clamp = (-100, 90) if case % 3 == 0 else None
+        graph, out = build(x, w, bias, zx, zw, pad, [1, 1], list(dil), rescale=rs, out_dtype=out_dtype, clamp=clamp)
+    check(graph, out, {"x": (x, "INT8")})
