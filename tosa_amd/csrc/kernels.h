@@ -87,10 +87,14 @@ struct ConvI8Desc {
     int32_t n = 1, ih = 1, iw = 1, ic = 1, oc = 1, kh = 1, kw = 1, oh = 1, ow = 1;
     int32_t pt = 0, pl = 0, sy = 1, sx = 1, dy = 1, dx = 1;
     int32_t zp_x = 0, zp_w = 0;
+    // DEPTHWISE_CONV2D with depth multiplier 1: w is [kh, kw, ic, 1] and
+    // oc == ic.
+    int32_t depthwise = 0;
 };
-// Geometry and alignment the kernel handles: 1x1 stride-1 unpadded
-// convolutions with ic % 16 == 0, any other geometry with ic % 64 == 0;
-// 16-byte aligned x and w.
+// Geometry and alignment the kernels handle: CONV2D 1x1 stride-1 unpadded
+// with ic % 16 == 0, any other CONV2D geometry with ic % 64 == 0;
+// DEPTHWISE_CONV2D with ic % 16 == 0 and at most 12 taps; 16-byte aligned
+// x (and w for CONV2D).
 bool conv_i8_fast_supported(const ConvI8Desc& d);
 // RESCALEs the fused epilogue handles: scale32 with SINGLE or DOUBLE
 // rounding, signed input with zero point 0 (the only legal one for int32).

@@ -684,6 +684,147 @@ __global__ void __launch_bounds__(HALO_NT, 2) conv_i8_halo_kernel(HaloArgs A)
                                  [&](int p) { return p < npix ? m0 + p : -1; });
 }
 
+// ---------------------------------------------------------------------------
+// DEPTHWISE_CONV2D (depth multiplier 1) on MFMA
+// ---------------------------------------------------------------------------
+// For 16 channels c0..c0+15 and 16 output pixels, the depthwise sum
+// out[c][p] = sum_t w[t][c] x~[p, t][c] is a 16 x 16 x (16 channels x 4 taps)
+// MFMA whose A operand is block-diagonal: lane (row c, k-chunk = tap t) holds
+// w[t][c] in byte c of its 16 bytes and zero elsewhere, and the B operand is
+// the plain 16-byte NHWC load of the channel group at (pixel, tap). Three
+// v_mfma_i32_16x16x64_i8 cover up to 12 taps (3x3 plus 3 zero taps); VALU
+// work is left to the epilogue alone. Zero points fold as in CONV2D with
+// K = taps: the per-channel terms come from the table, the per-(pixel,
+// channel) term zw sum_t x~ from a second MFMA against block-diagonal ones.
+//
+// A workgroup covers 64 consecutive output pixels (flattened n, oy, ox) and
+// 4 consecutive channel groups, one per wave, so that its waves read the same
+// input lines (L1 reuse) and each wave issues all its loads at once.
+struct DwArgs {
+    const int8_t* x;
+    const int8_t* w;
+    const v4i* tab;
+    int32_t P, C, IH, IW, OH, OW, KW, T, sy, sx, dy, dx, pt, pl;
+    FastDiv div_ohow, div_ow;
+    int32_t zp_x;
+    EpiArgs E;
+};
+
+template <int G, int OB, bool RS, bool ZW>
+__global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
+{
+    constexpr int TN = 4;  // 16-pixel tiles per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int j16 = lane & 15;
+    const int grp = lane >> 4;
+    const int p0 = blockIdx.x * (16 * TN);
+    const uint32_t zf = uint32_t(uint8_t(A.zp_x)) * 0x01010101u;
+    const v4u zfill = v4u{zf, zf, zf, zf};
+
+    // Input offsets of this lane's pixel in each tile (without the tap) and
+    // the tap of each of its k-chunks: tap 4 g + grp of group g.
+    int32_t iy0[TN], ix0[TN], pbase[TN];
+    bool pok[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+        const int p = p0 + 16 * tn + j16;
+        pok[tn] = p < A.P;
+        const int pp = pok[tn] ? p : 0;
+        const int b = fdiv(pp, A.div_ohow);
+        const int rem = pp - b * (A.OH * A.OW);
+        const int oy = fdiv(rem, A.div_ow);
+        const int ox = rem - oy * A.OW;
+        iy0[tn] = oy * A.sy - A.pt;
+        ix0[tn] = ox * A.sx - A.pl;
+        pbase[tn] = b * A.IH * A.IW;
+    }
+    int32_t tdy[G], tdx[G];
+    bool tok[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int t = 4 * g + grp;
+        tok[g] = t < A.T;
+        const int ky = t / A.KW;
+        tdy[g] = ky * A.dy;
+        tdx[g] = (t - ky * A.KW) * A.dx;
+    }
+
+    const int cg = blockIdx.y * 4 + wave;
+    if (cg < (A.C >> 4)) {
+        const int c0 = cg * 16;
+        // Block-diagonal A fragments: byte j16 of 16 is w[t][c0 + j16].
+        v4i wa[G], wo[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const int t = 4 * g + grp;
+            const uint32_t wv = tok[g] ? uint32_t(uint8_t(A.w[t * A.C + c0 + j16])) : 0u;
+            const int sh = 8 * (j16 & 3);
+            const int wd = j16 >> 2;
+            wa[g] = v4i{wd == 0 ? int(wv << sh) : 0, wd == 1 ? int(wv << sh) : 0, wd == 2 ? int(wv << sh) : 0,
+                        wd == 3 ? int(wv << sh) : 0};
+            if constexpr (ZW) {
+                const uint32_t one = tok[g] ? 1u : 0u;
+                wo[g] = v4i{wd == 0 ? int(one << sh) : 0, wd == 1 ? int(one << sh) : 0,
+                            wd == 2 ? int(one << sh) : 0, wd == 3 ? int(one << sh) : 0};
+            }
+        }
+        // Table of the 4 output channels this lane holds: c0 + 4 grp + i.
+        v4i t0[4], t1[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            t0[i] = A.tab[2 * (c0 + 4 * grp + i)];
+            if constexpr (RS)
+                t1[i] = A.tab[2 * (c0 + 4 * grp + i) + 1];
+        }
+        bool bad_range = false;
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            v4i acc = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const int iy = iy0[tn] + tdy[g];
+                const int ix = ix0[tn] + tdx[g];
+                const bool ok = tok[g] && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
+                const v4u v = ld16(A.x + (ok ? (pbase[tn] + iy * A.IW + ix) * A.C + c0 : 0));
+                const v4i bx = __builtin_bit_cast(v4i, ok ? v : zfill);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, acc, 0, 0, 0);
+                if constexpr (ZW)
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc1, 0, 0, 0);
+            }
+            if (!pok[tn])
+                continue;
+            int32_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                int32_t xv = int32_t(uint32_t(acc[i]) + uint32_t(t0[i].x));
+                if constexpr (ZW)
+                    xv = int32_t(uint32_t(xv) - uint32_t(A.E.zp_w) * uint32_t(acc1[i]));
+                if constexpr (RS) {
+                    bad_range |= uint32_t((xv >> t0[i].z) + 1) > 1u;
+                    const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
+                    const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
+                    const int32_t r = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
+                    v[i] = med3(r + A.E.out_zp, A.E.clo, A.E.chi);
+                } else {
+                    v[i] = xv;
+                }
+            }
+            uint8_t* dst = A.E.out + (int64_t(p0 + 16 * tn + j16) * A.C + c0 + 4 * grp) * OB;
+            if constexpr (OB == 1)
+                *reinterpret_cast<uint32_t*>(dst) = (uint32_t(v[0]) & 0xFF) | ((uint32_t(v[1]) & 0xFF) << 8) |
+                                                    ((uint32_t(v[2]) & 0xFF) << 16) | (uint32_t(v[3]) << 24);
+            else if constexpr (OB == 2)
+                *reinterpret_cast<v2u*>(dst) = v2u{(uint32_t(v[0]) & 0xFFFF) | (uint32_t(v[1]) << 16),
+                                                   (uint32_t(v[2]) & 0xFFFF) | (uint32_t(v[3]) << 16)};
+            else
+                *reinterpret_cast<v4i*>(dst) = v4i{v[0], v[1], v[2], v[3]};
+        }
+        if (bad_range)
+            atomicOr(A.E.err, DERR_SCALE_RANGE);
+    }
+}
+
 // One wave per output channel:
 //   tab[2c]   = {bias + K zx zw - zx sum_k w[c][k] (mod 2^32), multiplier,
 //                min(shift - 1, 31), shift}
@@ -691,16 +832,17 @@ __global__ void __launch_bounds__(HALO_NT, 2) conv_i8_halo_kernel(HaloArgs A)
 //                rounding constant for values < 0 (int64, lo/hi)}
 // The rounding constants are apply_scale_32's 2^(s-1), plus or minus 2^30
 // under double rounding for shifts above 31 (src/ops/quant.rs:26-29).
-__global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, const int32_t* bias, int32_t bias_len,
-                                     int32_t zx, int32_t zw, const int32_t* mult, const int32_t* shift,
-                                     int32_t per_channel, int32_t dbl, v4i* tab)
+__global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int32_t cstride, int32_t kstride,
+                                     const int32_t* bias, int32_t bias_len, int32_t zx, int32_t zw,
+                                     const int32_t* mult, const int32_t* shift, int32_t per_channel, int32_t dbl,
+                                     v4i* tab)
 {
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
     int32_t s = 0;
     if (zx != 0)
         for (int k = lane; k < K; k += 64)
-            s += w[int64_t(c) * K + k];
+            s += w[int64_t(c) * cstride + int64_t(k) * kstride];
     for (int off = 32; off > 0; off >>= 1)
         s += __shfl_xor(s, off);
     if (lane != 0)
@@ -877,10 +1019,45 @@ bool halo_plan(const ConvI8Desc& d, bool zw, HaloArgs& a, int& bc, int& kc, size
     return true;
 }
 
+template <int G, int OB, bool RS, bool ZW>
+void launch_dw(const DwArgs& a, hipStream_t s)
+{
+    const unsigned blocks = unsigned((a.P + 63) / 64);
+    hipLaunchKernelGGL((conv_i8_dw_kernel<G, OB, RS, ZW>), dim3(blocks, unsigned((a.C / 16 + 3) / 4)), dim3(256), 0, s,
+                       a);
+}
+
+template <int G>
+void launch_dw_epi(const DwArgs& a, int ob, bool rs, bool zw, hipStream_t s)
+{
+    if (!rs) {
+        if (zw)
+            launch_dw<G, 4, false, true>(a, s);
+        else
+            launch_dw<G, 4, false, false>(a, s);
+        return;
+    }
+#define TOSA_DW_OB(OBV)                          \
+    if (zw)                                      \
+        launch_dw<G, OBV, true, true>(a, s);     \
+    else                                         \
+        launch_dw<G, OBV, true, false>(a, s);
+    if (ob == 1) {
+        TOSA_DW_OB(1)
+    } else if (ob == 2) {
+        TOSA_DW_OB(2)
+    } else {
+        TOSA_DW_OB(4)
+    }
+#undef TOSA_DW_OB
+}
+
 }  // namespace
 
 bool conv_i8_fast_supported(const ConvI8Desc& d)
 {
+    if (d.depthwise)
+        return d.ic % 16 == 0 && d.oc == d.ic && d.kh * d.kw <= 12 && reinterpret_cast<uintptr_t>(d.x) % 16 == 0;
     const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
                     d.iw == d.ow;
     const bool aligned = (reinterpret_cast<uintptr_t>(d.x) % 16 == 0) && (reinterpret_cast<uintptr_t>(d.w) % 16 == 0);
@@ -895,9 +1072,12 @@ void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStre
 {
     if (d.oc <= 0)
         return;
-    const int32_t K = d.kh * d.kw * d.ic;
-    hipLaunchKernelGGL(conv_i8_table_kernel, dim3(d.oc), dim3(64), 0, stream, d.w, d.oc, K, d.bias, d.bias_len,
-                       d.zp_x, d.zp_w, rs ? rs->mult : nullptr, rs ? rs->shift : nullptr,
+    // Weight element (channel c, reduction index k): OHWI w[c K + k]; depthwise
+    // [KH, KW, C, 1] w[k C + c].
+    const int32_t K = d.depthwise ? d.kh * d.kw : d.kh * d.kw * d.ic;
+    const int32_t cstride = d.depthwise ? 1 : K, kstride = d.depthwise ? d.ic : 1;
+    hipLaunchKernelGGL(conv_i8_table_kernel, dim3(d.oc), dim3(64), 0, stream, d.w, d.oc, K, cstride, kstride, d.bias,
+                       d.bias_len, d.zp_x, d.zp_w, rs ? rs->mult : nullptr, rs ? rs->shift : nullptr,
                        rs ? rs->per_channel : 0, rs ? int32_t(rs->rounding == 3) : 0, static_cast<v4i*>(tab));
 }
 
@@ -930,6 +1110,38 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)
         return;
     const bool zw = d.zp_w != 0;
+    if (d.depthwise) {
+        DwArgs w{};
+        w.x = d.x;
+        w.w = d.w;
+        w.tab = static_cast<const v4i*>(tab);
+        w.P = d.n * d.oh * d.ow;
+        w.C = d.ic;
+        w.IH = d.ih;
+        w.IW = d.iw;
+        w.OH = d.oh;
+        w.OW = d.ow;
+        w.KW = d.kw;
+        w.T = d.kh * d.kw;
+        w.sy = d.sy;
+        w.sx = d.sx;
+        w.dy = d.dy;
+        w.dx = d.dx;
+        w.pt = d.pt;
+        w.pl = d.pl;
+        w.div_ohow = FastDiv(uint32_t(d.oh * d.ow));
+        w.div_ow = FastDiv(uint32_t(d.ow));
+        w.zp_x = d.zp_x;
+        w.E = e;
+        const int groups = (w.T + 3) / 4;
+        if (groups == 1)
+            launch_dw_epi<1>(w, ob, rs != nullptr, zw, stream);
+        else if (groups == 2)
+            launch_dw_epi<2>(w, ob, rs != nullptr, zw, stream);
+        else
+            launch_dw_epi<3>(w, ob, rs != nullptr, zw, stream);
+        return;
+    }
     const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
                     d.iw == d.ow;
 

@@ -725,7 +725,11 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
     const int64_t K = g.kh * g.kw * (depthwise ? 1 : g.ic);
     const bool i8 = is_int && acc_t == DT_INT32 && in_t == DT_INT8;
     const bool mfma_int = i8 && !depthwise;
-    const bool dw_int = i8 && depthwise && g.m == 1 && depthwise_i8_supported(int(g.kh), int(g.kw), int(g.ic));
+    // int8 depthwise: the MFMA kernel (ic % 16 == 0, <= 12 taps) or the VALU
+    // kernel (ic % 4 == 0, small kernels).
+    const bool dw_int = i8 && depthwise && g.m == 1 &&
+                        (depthwise_i8_supported(int(g.kh), int(g.kw), int(g.ic)) ||
+                         (g.ic % 16 == 0 && g.kh * g.kw <= 12));
     const bool mfma_float = !is_int && !depthwise && !st.opts.strict_float && acc_t == DT_FP32 &&
                             ((in_t == DT_BF16 && w_t == DT_BF16) || (in_t == DT_FP16 && w_t == DT_FP16));
 
@@ -740,7 +744,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         const bool wb_const = st.const_defs.count(op.inputs[1]) && st.const_defs.count(op.inputs[2]);
         ConvI8Desc fd;
         bool fast = false;
-        if (mfma_int) {
+        if (mfma_int || dw_int) {
             fd.x = static_cast<const int8_t*>(x);
             fd.w = static_cast<const int8_t*>(w);
             fd.bias = static_cast<const int32_t*>(bias->data->device_in());
@@ -762,6 +766,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             fd.dx = int32_t(g.dx);
             fd.zp_x = int32_t(izp);
             fd.zp_w = int32_t(wzp);
+            fd.depthwise = depthwise ? 1 : 0;
             fast = conv_i8_fast_supported(fd);
         }
         // Per-channel weight sums for the generic kernel, needed when the
@@ -831,6 +836,16 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             if (fast && (!rs || conv_i8_fast_epilogue_ok(*rs))) {
                 auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), rs, wb_const && (!rs || rs_const), s);
                 conv_i8_fast(fd, tab->device_in(), rs, out, err, s);
+                return;
+            }
+            if (fast && !mfma_int && !depthwise_i8_supported(fd.kh, fd.kw, fd.ic)) {
+                // A RESCALE the fused epilogue does not take, on a depthwise
+                // shape only the MFMA kernel handles: int32 result, then the
+                // standalone RESCALE (+CLAMP) kernel.
+                auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), nullptr, wb_const, s);
+                auto tmp = make_device_storage(DT_INT32, int64_t(fd.n) * fd.oh * fd.ow * fd.oc);
+                conv_i8_fast(fd, tab->device_in(), nullptr, tmp->device_out(), err, s);
+                kern::rescale(*rs, E_I32, tmp->device_in(), tmp->count, out, err, s);
                 return;
             }
             if (mfma_int) {
