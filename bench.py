@@ -13,6 +13,13 @@ stream) and the CPU oracle timed on the host beside it; `extra` carries the
 other benchmark configurations (incl. the int8 MobileNetV2-style graph img/s).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+    python bench.py --only NAME [--copy-mib M]   # one workload, for profilers
+
+`--only` runs one workload of WORKLOADS (timing only, no CPU baseline) and
+`--copy-mib` appends device-to-device copies of M MiB (torch's copy kernel),
+whose FETCH_SIZE / WRITE_SIZE readings calibrate the HBM traffic counters.
+The conv kernel's HBM traffic per launch comes from those counter runs and is
+read from the `TRAFFIC` line of the committed profile summary.
 """
 
 import argparse
@@ -39,7 +46,42 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="headline workload only")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
+    p.add_argument("--only", default=None, help="run one workload (a WORKLOADS key) and print its timing")
+    p.add_argument("--copy-mib", type=int, default=0, help="with --only: also run device copies of this size")
     return p.parse_args()
+
+
+HEADLINE = "conv_rescale_64x28x28x128"
+HEADLINE_KERNEL = "conv_i8_halo_kernel"
+# name -> (builder name in tosa_amd.workloads, kwargs, count ops, steps override)
+WORKLOADS = {
+    HEADLINE: ("conv_rescale", dict(n=64, h=28, w=28, cin=128, cout=128), True, None),
+    "mobilenet_v2_int8_n64": ("mobilenet_v2", dict(n=64), True, None),
+    "cfg1_conv_rescale_1x56x56x64": ("conv_rescale", {}, True, None),
+    "conv_rescale_64x14x14x256": ("conv_rescale", dict(n=64, h=14, w=14, cin=256, cout=256), True, None),
+    "cfg2_matmul_rescale_8x512x1024x1024": ("matmul_rescale", {}, True, None),
+    "cfg3_depthwise_32x112x112x144_s2": ("depthwise", {}, True, None),
+    "cfg3_avg_pool_32x7x7x1280": ("avg_pool", {}, False, None),
+    "cfg5_bf16_conv3x3_64x28x28x128": ("float_conv", dict(dtype="BF16"), True, None),
+    "cfg5_fp16_conv3x3_64x28x28x128": ("float_conv", dict(dtype="FP16"), True, None),
+    "cfg5_bf16_conv1x1_64x28x28x128to512": ("float_conv", dict(dtype="BF16", cout=512, k=1), True, None),
+    "cfg5_bf16_matmul_16x2048x2048x2048": ("float_matmul", {}, True, 5),
+}
+
+
+def traffic_from_profile(kernel):
+    """HBM bytes per launch of `kernel` from the TRAFFIC line of the committed
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy)."""
+    path = os.path.join(ROOT, "profiles", "conv_i8_rescale_64x28x28x128.md")
+    try:
+        with open(path) as f:
+            for ln in f:
+                parts = ln.split()
+                if len(parts) == 3 and parts[0] == "TRAFFIC" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 class Runner:
@@ -148,6 +190,32 @@ def _oracle_conv_rescale(O, x, p):
     return y.vals.astype(np.int8).reshape(acc.shape)
 
 
+def run_only(args, torch, T, W, sleep):
+    """One workload, `--steps` timed runs after `--warmup`, then optionally
+    `--copy-mib` device copies: the command profilers wrap."""
+    if args.only not in WORKLOADS:
+        print(f"unknown workload {args.only!r}; choose one of {', '.join(WORKLOADS)}", file=sys.stderr)
+        sys.exit(2)
+    builder, kw, unit_ops, _ = WORKLOADS[args.only]
+    g, i, inf = getattr(W, builder)(**kw)
+    r = Runner(T, torch, g, i)
+    sec = r.wall(args.steps, args.warmup)
+    k = r.gpu_time(max(1, args.steps), sleep)
+    line = {"workload": args.only, "ms_per_step": sec * 1e3, "gpu_ms": k * 1e3, "GB_s": inf["bytes"] / k / 1e9}
+    if unit_ops:
+        line["TOPS"] = inf["ops"] / k / 1e12
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(max(1, args.steps)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_bytes_per_launch"] = {"read": n, "write": n}
+    print(json.dumps(line))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -171,6 +239,10 @@ def main():
     T.set_option("deferred", 1)
     sleep = calibrate_sleep(torch, 0.02)
 
+    if args.only is not None:
+        run_only(args, torch, T, W, sleep)
+        return
+
     # ---- headline: int8 CONV2D + RESCALE at ResNet conv3_x scale ----------
     graph, ins, info = W.conv_rescale(n=64, h=28, w=28, cin=128, cout=128)
     r = Runner(T, torch, graph, ins)
@@ -185,8 +257,9 @@ def main():
     extra = {"headline_image0_bit_exact_vs_oracle": bool(np.array_equal(out_img0, cpu_img0[0])),
              "headline_kernel_us": kern * 1e6}
 
-    def measure(name, builder, unit_ops=True, steps=None, **kw):
-        g, i, inf = builder(**kw)
+    def measure(name):
+        builder, kw, unit_ops, steps = WORKLOADS[name]
+        g, i, inf = getattr(W, builder)(**kw)
         rr = Runner(T, torch, g, i)
         s = rr.wall(steps or max(5, args.steps // 5), 2)
         k = rr.gpu_time(5, sleep)
@@ -198,18 +271,12 @@ def main():
         return inf, s, k
 
     if not args.quick:
-        inf, s, k = measure("mobilenet_v2_int8_n64", W.mobilenet_v2, n=64)
+        inf, s, k = measure("mobilenet_v2_int8_n64")
         extra["mobilenet_v2_int8_n64"].update({"img_s": 64 / s, "img_s_gpu": 64 / k,
                                                "hbm_roofline_frac": inf["bytes"] / k / 1e9 / PEAK_HBM_GBS})
-        measure("cfg1_conv_rescale_1x56x56x64", W.conv_rescale)
-        measure("conv_rescale_64x14x14x256", W.conv_rescale, n=64, h=14, w=14, cin=256, cout=256)
-        measure("cfg2_matmul_rescale_8x512x1024x1024", W.matmul_rescale)
-        measure("cfg3_depthwise_32x112x112x144_s2", W.depthwise)
-        measure("cfg3_avg_pool_32x7x7x1280", W.avg_pool, unit_ops=False)
-        measure("cfg5_bf16_conv3x3_64x28x28x128", W.float_conv, dtype="BF16")
-        measure("cfg5_fp16_conv3x3_64x28x28x128", W.float_conv, dtype="FP16")
-        measure("cfg5_bf16_conv1x1_64x28x28x128to512", W.float_conv, dtype="BF16", cout=512, k=1)
-        measure("cfg5_bf16_matmul_16x2048x2048x2048", W.float_matmul, steps=5)
+        for name in WORKLOADS:
+            if name not in (HEADLINE, "mobilenet_v2_int8_n64"):
+                measure(name)
 
     line = {
         "metric": METRIC,
@@ -228,7 +295,7 @@ def main():
                                "RESCALE->int8 (zx=-3, zw=0, output zp 5)",
                    "global_batch": 64, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
-                     "frac": achieved / PEAK_INT8_TOPS, "traffic": None},
+                     "frac": achieved / PEAK_INT8_TOPS, "traffic": traffic_from_profile(HEADLINE_KERNEL)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

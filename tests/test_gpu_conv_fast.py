@@ -203,6 +203,10 @@ HALO = [
     (1, 28, 28, 512, 96, 3, 3, (1, 1), (1, 1, 1, 1)),
     (1, 29, 31, 64, 200, 2, 2, (1, 2), (0, 1, 1, 0)),
     (3, 16, 16, 320, 24, 3, 3, (2, 2), (2, 2, 2, 2)),
+    (2, 12, 12, 32, 48, 3, 3, (1, 1), (1, 1, 1, 1)),
+    (1, 9, 40, 96, 136, 3, 3, (1, 1), (1, 1, 1, 1)),
+    (1, 5, 250, 32, 32, 1, 3, (1, 1), (0, 0, 1, 1)),
+    (1, 14, 14, 160, 256, 3, 3, (1, 1), (0, 2, 1, 1)),
 ]
 
 

@@ -90,6 +90,9 @@ struct ConvI8Desc {
     // DEPTHWISE_CONV2D with depth multiplier 1: w is [kh, kw, ic, 1] and
     // oc == ic.
     int32_t depthwise = 0;
+    // Weights packed by conv_i8_wpack (when conv_i8_wpack_bytes > 0); the
+    // stride-1 halo kernel runs only with them.
+    const int8_t* wpack = nullptr;
 };
 // Geometry and alignment the kernels handle: CONV2D 1x1 stride-1 unpadded
 // with ic % 16 == 0, any other CONV2D geometry with ic % 64 == 0;
@@ -99,11 +102,17 @@ bool conv_i8_fast_supported(const ConvI8Desc& d);
 // RESCALEs the fused epilogue handles: scale32 with SINGLE or DOUBLE
 // rounding, signed input with zero point 0 (the only legal one for int32).
 bool conv_i8_fast_epilogue_ok(const RescaleDev& rs);
-// Per-channel epilogue table (8 int32 per output channel) built on the
+// Per-channel epilogue table (8 int32 per output channel, then 4 int32 of
+// the input zero point's byte, then one int32 per channel) built on the
 // device from w, bias, the zero points and, when `rs` is given, the RESCALE
 // multiplier and shift.
 constexpr int CONV_I8_TABLE_WORDS = 8;
+inline int64_t conv_i8_table_words(int32_t oc) { return int64_t(CONV_I8_TABLE_WORDS + 1) * oc + 4; }
 void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStream_t stream);
+// Bytes of the packed weight layout of the stride-1 halo kernel for `d`, 0
+// when that kernel does not run for `d`; conv_i8_wpack writes it from d.w.
+int64_t conv_i8_wpack_bytes(const ConvI8Desc& d);
+void conv_i8_wpack(const ConvI8Desc& d, void* wp, hipStream_t stream);
 // The convolution; `rs` selects the fused RESCALE (+CLAMP) epilogue with the
 // table built for the same `rs`, else the int32 output (conv + bias).
 void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,

@@ -125,8 +125,8 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
                 if constexpr (RS) {
                     // apply_scale_32: the value must lie in [-2^(s-1), 2^(s-1)),
                     // a condition on int32 values only for shifts below 32
-                    // (t0.z = min(s - 1, 31)).
-                    bad_range |= uint32_t((x >> t0[i].z) + 1) > 1u;
+                    // (t0.z = -2^min(s - 1, 31), ~t0.z = 2^min(s - 1, 31) - 1).
+                    bad_range |= med3(x, t0[i].z, ~t0[i].z) != x;
                     const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                     const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                     // With the value in range and 0 <= multiplier < 2^31 the
@@ -685,6 +685,449 @@ __global__ void __launch_bounds__(HALO_NT, 2) conv_i8_halo_kernel(HaloArgs A)
 }
 
 // ---------------------------------------------------------------------------
+// Stride-1 convolution on v_mfma_i32_32x32x32_i8 with the input halo and the
+// weights streamed through LDS.
+//
+// A workgroup computes BC output channels x up to 256 consecutive output
+// pixels of one image (R whole output rows) with BC / 16 waves: wave w owns
+// channels 64 (w / 4) .. + 63 (two 32-channel tiles) of the 32-pixel tiles
+// w % 4 and w % 4 + 4, so one weight fragment feeds two MFMAs and so does
+// one pixel fragment. Two waves per SIMD (BC = 128) keep each wave's LDS
+// reads (4 KB per tap) within what one wave can draw from LDS while the
+// SIMD's MFMAs run back to back.
+//
+// K is walked as (32-channel pass, tap). The halo (R + (KH-1) dy rows of
+// OW + (KW-1) dx positions) is staged 64 input channels at a time in a ring
+// of two LDS buffers, each position's 64 bytes loaded by 4 lanes; the
+// weights of a pass (every tap) sit in one of two LDS buffers. While a pass
+// is multiplied, the next pass's weights (and, at the first pass of a
+// stage, the next stage's halo) are fetched by direct global->LDS loads.
+// The weights come pre-packed in exactly their LDS image
+// ([block][pass][tap][channel tile][lane][16 bytes]), so each of those loads
+// reads 1 KB of contiguous memory.
+//
+// MFMA operand layout (checked on the device): lane l supplies row l % 32 of
+// A and column l % 32 of B, both with the 16 bytes of k-half l / 32; result
+// element i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
+// A = weights, B = pixels. Weight rows are permuted, row r <- channel
+// 16 ((r >> 2) & 1) + 4 (r >> 3) + (r & 3), so that result element i of lane
+// l is channel 16 (l / 32) + i: each lane ends with 16 consecutive channels
+// of one pixel per tile, stored as one vector. The accumulators start at the
+// channel's additive constant (bias and zero-point terms).
+//
+// Halo stage layout: [position hp][4 chunks of 16 bytes], chunk c stored at
+// c ^ ((hp >> 2) & 3), so that 16 consecutive positions reading one logical
+// chunk hit 16 distinct bank groups. Padding taps (and channels past IC in
+// a 32-channel last stage) are loaded from 16 bytes of the input zero point
+// stored after the table.
+// ---------------------------------------------------------------------------
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct Halo32Args {
+    const int8_t* x;
+    const int8_t* wp;  // packed weights
+    const v4i* tab;    // [N][2] entries, 16 bytes of the input zero point, [N] additive constants
+    int32_t N, IC, IH, IW, OH, OW, KW, taps, dy, dx, pt, pl;
+    int32_t R, tiles_per_img, HR, HW;
+    int32_t sbytes;  // LDS bytes of one halo stage (HR*HW*64, 1 KB multiple)
+    int32_t wbytes;  // bytes of one pass's weights (taps * BC * 32)
+    FastDiv div_ow, div_hw;
+    EpiArgs E;
+};
+
+constexpr int H32_TB = 2;                // 32-pixel tiles per wave
+constexpr int H32_BP = 4 * 32 * H32_TB;  // pixel slots per workgroup
+
+// A direct 16-byte global->LDS load (global_load_lds_dwordx4: lane l writes
+// LDS byte address `l` + 16 l, `l` wave-uniform). Issued through inline
+// assembly: LLVM's wait-count pass counts a builtin LDS DMA in flight as an
+// out-of-order LDS event and then makes every LDS read wait for all earlier
+// ones (lgkmcnt(0)), which serialises the fragment prefetch. The callers wait
+// for these loads themselves (s_waitcnt vmcnt(0) and a barrier) before
+// reading what they fill.
+__device__ __forceinline__ void dma16(const void* g, const void* l)
+{
+    const uint32_t la = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((const lvoid*)l)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(la) : "memory", "m0");
+}
+
+// Weight row of MFMA row r (see above).
+__device__ __forceinline__ int h32_row_channel(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
+
+// Epilogue of the 32x32 layout: lane (h, l32) holds channels 32 a + 16 h +
+// 0..15 (counted from n0; s_tab starts at channel n0) of tile pixel
+// 32 (pw + 4 b) + l32 in acc[a][b], the channel's additive constant already
+// included.
+template <int TA, int TB, int OB, bool RS, bool ZW, typename PixelMap>
+__device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab, const int32_t* s_rowsum, int n0,
+                                           int pw, int lane, const EpiArgs& E, PixelMap pixel)
+{
+    const int l32 = lane & 31, h = lane >> 5;
+    // Nonzero when a value fails apply_scale_32's range REQUIRE (VALU
+    // accumulation: one bitwise op per value, no scalar round trips).
+    uint32_t bad_bits = 0;
+    int32_t zwx[TB];
+    int64_t m[TB];
+#pragma unroll
+    for (int b = 0; b < TB; b++) {
+        const int p = 32 * (pw + 4 * b) + l32;
+        m[b] = pixel(p);
+        zwx[b] = 0;
+        if constexpr (ZW)
+            zwx[b] = int32_t(uint32_t(E.zp_w) * uint32_t(s_rowsum[p]));
+    }
+#pragma unroll
+    for (int a = 0; a < TA; a++) {
+        const int cl = 32 * a + 16 * h;  // tile channel of element 0
+        uint32_t res[TB][4 * OB];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            __builtin_amdgcn_sched_barrier(0);
+            v4i t0[4], t1[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                t0[i] = s_tab[2 * (cl + 4 * g + i)];
+                if constexpr (RS)
+                    t1[i] = s_tab[2 * (cl + 4 * g + i) + 1];
+            }
+#pragma unroll
+            for (int b = 0; b < TB; b++) {
+                __builtin_amdgcn_sched_barrier(0);
+                int32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int32_t x = int32_t(uint32_t(acc[a][b][4 * g + i]) - uint32_t(zwx[b]));
+                    if constexpr (RS) {
+                        // Same arithmetic as epilogue(): range REQUIRE of
+                        // apply_scale_32, 64-bit scale with the per-sign
+                        // rounding constant, output zero point and clamp.
+                        bad_bits |= uint32_t(med3(x, t0[i].z, ~t0[i].z)) ^ uint32_t(x);
+                        const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
+                        const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
+                        const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
+                        v[i] = med3(r + E.out_zp, E.clo, E.chi);
+                    } else {
+                        v[i] = x;
+                    }
+                }
+                if constexpr (OB == 1) {
+                    res[b][g] = (uint32_t(v[0]) & 0xFF) | ((uint32_t(v[1]) & 0xFF) << 8) |
+                                ((uint32_t(v[2]) & 0xFF) << 16) | (uint32_t(v[3]) << 24);
+                } else if constexpr (OB == 2) {
+                    res[b][2 * g] = (uint32_t(v[0]) & 0xFFFF) | (uint32_t(v[1]) << 16);
+                    res[b][2 * g + 1] = (uint32_t(v[2]) & 0xFFFF) | (uint32_t(v[3]) << 16);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        res[b][4 * g + i] = uint32_t(v[i]);
+                }
+#pragma unroll
+                for (int wd = 0; wd < OB; wd++)
+                    asm volatile("" : "+v"(res[b][g * OB + wd]));
+                // Kept as a vector value (left alone, the compiler turns the
+                // accumulation into compares and scalar ORs, a VALU -> SALU
+                // dependency per value).
+                if constexpr (RS)
+                    asm volatile("" : "+v"(bad_bits));
+            }
+        }
+        const int c0 = n0 + cl;
+#pragma unroll
+        for (int b = 0; b < TB; b++) {
+            if (m[b] < 0)
+                continue;
+            const int64_t o = m[b] * E.N + c0;
+            uint8_t* dst = E.out + o * OB;
+            if (c0 + 16 <= E.N && ((o * OB) & 15) == 0) {
+#pragma unroll
+                for (int wd = 0; wd < 4 * OB; wd += 4)
+                    *reinterpret_cast<v4u*>(dst + 4 * wd) =
+                        v4u{res[b][wd], res[b][wd + 1], res[b][wd + 2], res[b][wd + 3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    if (c0 + e >= E.N)
+                        continue;
+                    const uint32_t word = res[b][(e * OB) / 4];
+                    const int sh = 8 * ((e * OB) % 4);
+                    if constexpr (OB == 1)
+                        dst[e] = uint8_t(word >> sh);
+                    else if constexpr (OB == 2)
+                        reinterpret_cast<uint16_t*>(dst)[e] = uint16_t(word >> sh);
+                    else
+                        reinterpret_cast<uint32_t*>(dst)[e] = word;
+                }
+            }
+        }
+    }
+    if (bad_bits)
+        atomicOr(E.err, DERR_SCALE_RANGE);
+}
+
+// KT: taps when fixed at compile time (9 = 3x3; the tap loop is then fully
+// unrolled so that each tap waits only for its own fragments), 0 = any.
+template <int BC, int KT, int OB, bool RS, bool ZW>
+__global__ void __launch_bounds__(BC * 4, 2) conv_i8_halo32_kernel(Halo32Args A)
+{
+    constexpr int NT = BC * 4;  // threads: 4 waves per 64 channels
+    constexpr int TA = 2;       // 32-channel tiles per wave
+    constexpr int TB = H32_TB;  // 32-pixel tiles per wave
+    constexpr int BP = H32_BP;
+
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t* const halo = smem;                                          // [2][sbytes]
+    uint8_t* const wbuf = smem + 2 * A.sbytes;                           // [2][wbytes]
+    v4i* const s_tab = reinterpret_cast<v4i*>(wbuf + 2 * A.wbytes);     // [2 BC]
+    int32_t* const s_hsum = reinterpret_cast<int32_t*>(s_tab + 2 * BC);  // ZW: [HR HW]
+    int32_t* const s_rowsum = s_hsum + A.HR * A.HW;                      // ZW: [BP]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int pw = wave & 3;        // pixel tiles pw, pw + 4
+    const int cw = 64 * (wave >> 2);  // first channel of the wave (tile-relative)
+    const int l32 = lane & 31;
+    const int h = lane >> 5;
+    const int img = blockIdx.x / A.tiles_per_img;
+    const int oy0 = (blockIdx.x - img * A.tiles_per_img) * A.R;
+    const int rows = A.OH - oy0 < A.R ? A.OH - oy0 : A.R;
+    const int npix = rows * A.OW;
+    const int n0 = blockIdx.y * BC;
+    const int hw = A.HR * A.HW;
+    const int taps = KT > 0 ? KT : A.taps;
+    const int passes = A.IC >> 5;
+
+    // Epilogue table straight into LDS (channels past N repeat channel N-1).
+    if (tid < 2 * BC) {
+        const int c = n0 + (tid >> 1);
+        dma16(A.tab + 2 * (c < A.N ? c : A.N - 1) + (tid & 1), s_tab + wave * 64);
+    }
+    if constexpr (ZW)
+        for (int i = tid; i < hw; i += NT)
+            s_hsum[i] = 0;
+
+    // Additive constants of this lane's channels (cw + 32 a + 16 h + i for
+    // result element i), fetched now and moved into the accumulators once
+    // the first loads have landed.
+    v16i acc[TA][TB], init[TA];
+    {
+        const int32_t* adds = reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1);
+#pragma unroll
+        for (int a = 0; a < TA; a++) {
+            const int c = n0 + cw + 32 * a + 16 * h;
+            if (c + 16 <= A.N) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4i v = *reinterpret_cast<const v4i*>(adds + c + 4 * q);
+                    init[a][4 * q] = v.x;
+                    init[a][4 * q + 1] = v.y;
+                    init[a][4 * q + 2] = v.z;
+                    init[a][4 * q + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    init[a][i] = adds[c + i < A.N ? c + i : A.N - 1];
+            }
+        }
+    }
+
+    // Halo position (tap 0) of this lane's pixel in each tile; pixels past
+    // the tile's end read pixel 0 and are not stored.
+    int32_t hpos[TB];
+#pragma unroll
+    for (int b = 0; b < TB; b++) {
+        const int p = 32 * (pw + 4 * b) + l32;
+        const int pp = p < npix ? p : 0;
+        const int r = fdiv(pp, A.div_ow);
+        hpos[b] = r * A.HW + pp - r * A.OW;
+    }
+
+    const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.IC;
+    const int8_t* const zfill = reinterpret_cast<const int8_t*>(A.tab + 2 * A.N);
+    const int8_t* const wsrc = A.wp + int64_t(blockIdx.y) * passes * A.wbytes + lane * 16;
+    const int nwq = taps * (BC / 32);  // 1 KB groups of one pass's weights
+    auto dma_w = [&](int pass) {
+        const int8_t* src = wsrc + int64_t(pass) * A.wbytes;
+        uint8_t* dst = wbuf + (pass & 1) * A.wbytes;
+        for (int j = wave; j < nwq; j += NT / 64)
+            dma16(src + j * 1024, dst + j * 1024);
+    };
+    // Halo stage st (input channels 64 st ..): 16-byte slot s of the LDS
+    // image is chunk s % 4 of position s / 4, stored swizzled; slots past the
+    // image (the last group's tail) load the zero-point fill into padding.
+    auto dma_halo = [&](int st) {
+        const int total = hw * 4;
+        const int ch0 = 64 * st;
+        uint8_t* const dst = halo + (st & 1) * A.sbytes;
+        for (int s0 = wave * 64; s0 < total; s0 += NT) {
+            const int sl = s0 + lane;
+            const int hp = sl >> 2;
+            const int c = (sl & 3) ^ ((hp >> 2) & 3);
+            const int hr = fdiv(hp, A.div_hw);
+            const int iy = oy0 - A.pt + hr;
+            const int ix = hp - hr * A.HW - A.pl;
+            const bool ok = sl < total && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW) &&
+                            ch0 + 16 * c < A.IC;
+            dma16(ok ? xi + (iy * A.IW + ix) * A.IC + ch0 + 16 * c : zfill, dst + s0 * 16);
+        }
+    };
+
+    dma_halo(0);
+    dma_w(0);
+    for (int pass = 0; pass < passes; pass++) {
+        // The loads of this pass (issued one pass earlier, or above) have
+        // landed, and every wave is done with the buffers the next loads
+        // overwrite.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (pass == 0) {
+#pragma unroll
+            for (int a = 0; a < TA; a++)
+#pragma unroll
+                for (int b = 0; b < TB; b++)
+                    acc[a][b] = init[a];
+        }
+        const int st = pass >> 1;
+        if ((pass & 1) == 0 && 2 * (st + 1) < passes)
+            dma_halo(st + 1);
+        if (pass + 1 < passes)
+            dma_w(pass + 1);
+        if constexpr (ZW) {
+            if ((pass & 1) == 0) {
+                const uint8_t* hs = halo + (st & 1) * A.sbytes;
+                for (int hp = tid; hp < hw; hp += NT) {
+                    int32_t t = s_hsum[hp];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        if (64 * st + 16 * c >= A.IC)
+                            break;  // zero-point fill past the last channel
+                        const v4u v = *reinterpret_cast<const v4u*>(hs + (hp * 4 + (c ^ ((hp >> 2) & 3))) * 16);
+                        t = __builtin_amdgcn_sdot4(int(v.x), 0x01010101, t, false);
+                        t = __builtin_amdgcn_sdot4(int(v.y), 0x01010101, t, false);
+                        t = __builtin_amdgcn_sdot4(int(v.z), 0x01010101, t, false);
+                        t = __builtin_amdgcn_sdot4(int(v.w), 0x01010101, t, false);
+                    }
+                    s_hsum[hp] = t;
+                }
+            }
+        }
+        const uint8_t* const wb = wbuf + (pass & 1) * A.wbytes + lane * 16;
+        const uint8_t* const hb = halo + (st & 1) * A.sbytes;
+        const int cl = 2 * (pass & 1) + h;  // logical chunk of this lane's k-half
+        // The fragments of tap t + 1 are read while tap t's MFMAs run.
+        auto load = [&](v4i(&fa)[TA], v4i(&fb)[TB], int t, int ky, int kx) {
+#pragma unroll
+            for (int a = 0; a < TA; a++)
+                fa[a] = *reinterpret_cast<const v4i*>(wb + (t * (BC / 32) + cw / 32 + a) * 1024);
+            const int off = ky * A.dy * A.HW + kx * A.dx;
+#pragma unroll
+            for (int b = 0; b < TB; b++) {
+                const int hp = hpos[b] + off;
+                fb[b] = *reinterpret_cast<const v4i*>(hb + (hp * 4 + (cl ^ ((hp >> 2) & 3))) * 16);
+            }
+        };
+        auto mfma = [&](const v4i(&fa)[TA], const v4i(&fb)[TB]) {
+#pragma unroll
+            for (int b = 0; b < TB; b++)
+#pragma unroll
+                for (int a = 0; a < TA; a++)
+                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], acc[a][b], 0, 0, 0);
+        };
+        if constexpr (KT == 9) {
+            v4i fa[2][TA], fb[2][TB];
+            load(fa[0], fb[0], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 9; t++) {
+                // Scheduling fences keep the next tap's reads ahead of this
+                // tap's MFMAs (left alone, the scheduler sinks them below the
+                // MFMAs to save registers, and the reads' latency shows).
+                __builtin_amdgcn_sched_barrier(0);
+                if (t + 1 < 9)
+                    load(fa[(t + 1) & 1], fb[(t + 1) & 1], t + 1, (t + 1) / 3, (t + 1) % 3);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma(fa[t & 1], fb[t & 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            int ky = 0, kx = 0;
+            auto step = [&]() {
+                if (++kx == A.KW) {
+                    kx = 0;
+                    ky++;
+                }
+            };
+            v4i fa0[TA], fb0[TB], fa1[TA], fb1[TB];
+            load(fa0, fb0, 0, 0, 0);
+            step();
+            for (int t = 0; t < taps; t += 2) {
+                const bool two = t + 1 < taps;
+                if (two) {
+                    load(fa1, fb1, t + 1, ky, kx);
+                    step();
+                }
+                mfma(fa0, fb0);
+                if (two) {
+                    if (t + 2 < taps) {
+                        load(fa0, fb0, t + 2, ky, kx);
+                        step();
+                    }
+                    mfma(fa1, fb1);
+                }
+            }
+        }
+    }
+
+    if constexpr (ZW) {
+        __syncthreads();  // every stage's sums are in
+        for (int p = tid; p < BP; p += NT) {
+            int32_t t = 0;
+            if (p < npix) {
+                const int r = fdiv(p, A.div_ow);
+                const int ox = p - r * A.OW;
+                for (int t2 = 0; t2 < taps; t2++) {
+                    const int ky2 = t2 / A.KW, kx2 = t2 - ky2 * A.KW;
+                    t += s_hsum[(r + ky2 * A.dy) * A.HW + ox + kx2 * A.dx];
+                }
+            }
+            s_rowsum[p] = t;
+        }
+        __syncthreads();
+    }
+
+    const int m0 = (img * A.OH + oy0) * A.OW;
+    epilogue32<TA, TB, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
+                                   [&](int p) { return p < npix ? m0 + p : -1; });
+}
+
+// Packed weights of the 32x32 halo kernel: 16-byte slot
+// ((((nb passes + p) taps + t) TA + a) 64 + l) holds bytes 32 p + 16 (l / 32)
+// .. + 15 of tap t of channel nb BC + 32 a + row_channel(l % 32) (zero past
+// N), i.e. every pass of every channel block is the LDS image its loads fill.
+__global__ void conv_i8_wpack_kernel(const int8_t* w, int32_t N, int32_t K, int32_t IC, int32_t taps, int32_t BC,
+                                     int64_t slots, v4u* out)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= slots)
+        return;
+    const int TA = BC / 32, passes = IC / 32;
+    int64_t r = i;
+    const int l = int(r % 64);
+    r /= 64;
+    const int a = int(r % TA);
+    r /= TA;
+    const int t = int(r % taps);
+    r /= taps;
+    const int p = int(r % passes);
+    const int nb = int(r / passes);
+    const int c = nb * BC + 32 * a + h32_row_channel(l % 32);
+    v4u v = v4u{0, 0, 0, 0};
+    if (c < N)
+        v = *reinterpret_cast<const v4u*>(w + int64_t(c) * K + t * IC + 32 * p + 16 * (l / 32));
+    out[i] = v;
+}
+
+// ---------------------------------------------------------------------------
 // DEPTHWISE_CONV2D (depth multiplier 1) on MFMA
 // ---------------------------------------------------------------------------
 // For 16 channels c0..c0+15 and 16 output pixels, the depthwise sum
@@ -801,7 +1244,7 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
                 if constexpr (ZW)
                     xv = int32_t(uint32_t(xv) - uint32_t(A.E.zp_w) * uint32_t(acc1[i]));
                 if constexpr (RS) {
-                    bad_range |= uint32_t((xv >> t0[i].z) + 1) > 1u;
+                    bad_range |= med3(xv, t0[i].z, ~t0[i].z) != xv;
                     const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                     const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                     const int32_t r = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
@@ -827,11 +1270,13 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
 
 // One wave per output channel:
 //   tab[2c]   = {bias + K zx zw - zx sum_k w[c][k] (mod 2^32), multiplier,
-//                min(shift - 1, 31), shift}
+//                -2^min(shift - 1, 31), shift}
 //   tab[2c+1] = {rounding constant for values >= 0 (int64, lo/hi),
 //                rounding constant for values < 0 (int64, lo/hi)}
-// The rounding constants are apply_scale_32's 2^(s-1), plus or minus 2^30
-// under double rounding for shifts above 31 (src/ops/quant.rs:26-29).
+// then, after the N channels, 16 bytes of the input zero point and the N
+// additive constants (tab[2c].x) as a dense array. The
+// rounding constants are apply_scale_32's 2^(s-1), plus or minus 2^30 under
+// double rounding for shifts above 31 (src/ops/quant.rs:26-29).
 __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int32_t cstride, int32_t kstride,
                                      const int32_t* bias, int32_t bias_len, int32_t zx, int32_t zw,
                                      const int32_t* mult, const int32_t* shift, int32_t per_channel, int32_t dbl,
@@ -839,6 +1284,10 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
 {
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
+    if (c == 0 && lane == 0) {
+        const int32_t zf = int32_t(uint32_t(uint8_t(zx)) * 0x01010101u);
+        tab[2 * N] = v4i{zf, zf, zf, zf};
+    }
     int32_t s = 0;
     if (zx != 0)
         for (int k = lane; k < K; k += 64)
@@ -858,7 +1307,11 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
     const int64_t half = int64_t(1) << (sh - 1);
     const int64_t d = (dbl && sh > 31) ? (int64_t(1) << 30) : 0;
     const int64_t rp = half + d, rn = half - d;
-    tab[2 * c] = v4i{int32_t(add), m, sh - 1 < 31 ? sh - 1 : 31, sh};
+    // Range bound of apply_scale_32's REQUIRE: values in [lo, ~lo] with
+    // lo = -2^min(s - 1, 31).
+    const int32_t lo = sh - 1 < 31 ? -(int32_t(1) << (sh - 1)) : INT32_MIN;
+    tab[2 * c] = v4i{int32_t(add), m, lo, sh};
+    reinterpret_cast<int32_t*>(tab + 2 * N + 1)[c] = int32_t(add);
     tab[2 * c + 1] = v4i{int32_t(uint32_t(uint64_t(rp))), int32_t(uint64_t(rp) >> 32),
                          int32_t(uint32_t(uint64_t(rn))), int32_t(uint64_t(rn) >> 32)};
 }
@@ -1019,6 +1472,130 @@ bool halo_plan(const ConvI8Desc& d, bool zw, HaloArgs& a, int& bc, int& kc, size
     return true;
 }
 
+template <int BC, int KT, int OB, bool RS, bool ZW>
+void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t s)
+{
+    auto kfn = conv_i8_halo32_kernel<BC, KT, OB, RS, ZW>;
+    static bool attr = [&]() {
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      HALO_LDS_MAX),
+                  "conv_i8 halo32 LDS size");
+        return true;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL(kfn, dim3(blocks, (a.N + BC - 1) / BC), dim3(BC * 4), lds, s, a);
+}
+
+template <int BC, int KT>
+void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob, bool rs, bool zw, hipStream_t s)
+{
+    if (!rs) {
+        if (zw)
+            launch_halo32<BC, KT, 4, false, true>(a, blocks, lds, s);
+        else
+            launch_halo32<BC, KT, 4, false, false>(a, blocks, lds, s);
+        return;
+    }
+#define TOSA_HALO32_OB(OBV)                                       \
+    if (zw)                                                       \
+        launch_halo32<BC, KT, OBV, true, true>(a, blocks, lds, s); \
+    else                                                          \
+        launch_halo32<BC, KT, OBV, true, false>(a, blocks, lds, s);
+    if (ob == 1) {
+        TOSA_HALO32_OB(1)
+    } else if (ob == 2) {
+        TOSA_HALO32_OB(2)
+    } else {
+        TOSA_HALO32_OB(4)
+    }
+#undef TOSA_HALO32_OB
+}
+
+// Compute units of the current device (workgroups of the 32x32 halo kernel
+// that run at once: its LDS allows one per CU).
+int cu_count()
+{
+    static int counts[64] = {0};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64)
+        return 256;
+    if (counts[dev] == 0) {
+        int n = 0;
+        hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+        counts[dev] = n > 0 ? n : 256;
+    }
+    return counts[dev];
+}
+
+// Geometry of the 32x32 halo kernel for `d`, or false when it does not
+// apply: stride 1, ic a multiple of 32, output rows of at most 256 pixels,
+// tiles of at least 96 pixels and buffers within the LDS. The rows per tile
+// R minimise (workgroup rounds, one workgroup per CU) x (pixel tiles of the
+// busiest wave + 1), the 1 standing for a tile's fixed cost (first loads,
+// epilogue).
+bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& lds, unsigned& blocks)
+{
+    if (d.sy != 1 || d.sx != 1 || d.ic % 32 != 0 || d.ow > H32_BP || d.oh < 1 || d.ow < 1 || d.depthwise)
+        return false;
+    bc = d.oc > 64 ? 128 : 64;
+    const int taps = d.kh * d.kw;
+    const int HW = d.ow + (d.kw - 1) * d.dx;
+    auto lds_for = [&](int R) {
+        const size_t hw = (size_t(R) + size_t(d.kh - 1) * d.dy) * HW;
+        size_t b = 2 * ((hw * 64 + 1023) / 1024 * 1024) + 2 * size_t(taps) * bc * 32 + size_t(32) * bc;
+        if (zw)
+            b += size_t(4) * (hw + H32_BP);
+        return b;
+    };
+    const int rmax = d.oh < H32_BP / d.ow ? d.oh : H32_BP / d.ow;
+    const long chb = (d.oc + bc - 1) / bc;
+    const long cus = cu_count();
+    int R = 0;
+    long best = 0;
+    for (int r = rmax; r >= 1; r--) {
+        if (r * d.ow < 96 && r != d.oh)
+            break;
+        if (lds_for(r) > size_t(HALO_LDS_MAX))
+            continue;
+        const long tiles = (r * d.ow + 31) / 32;
+        const long per_wave = (tiles + 3) / 4;
+        const long nb = long(d.n) * ((d.oh + r - 1) / r) * chb;
+        const long cost = (nb + cus - 1) / cus * (per_wave + 1);
+        if (R == 0 || cost < best) {
+            R = r;
+            best = cost;
+        }
+    }
+    if (R == 0 || R * d.ow < 96)
+        return false;
+    a.x = d.x;
+    a.wp = d.wpack;
+    a.N = d.oc;
+    a.IC = d.ic;
+    a.IH = d.ih;
+    a.IW = d.iw;
+    a.OH = d.oh;
+    a.OW = d.ow;
+    a.KW = d.kw;
+    a.taps = taps;
+    a.dy = d.dy;
+    a.dx = d.dx;
+    a.pt = d.pt;
+    a.pl = d.pl;
+    a.R = R;
+    a.tiles_per_img = (d.oh + R - 1) / R;
+    a.HR = R + (d.kh - 1) * d.dy;
+    a.HW = HW;
+    a.sbytes = int32_t((size_t(a.HR) * HW * 64 + 1023) / 1024 * 1024);
+    a.wbytes = taps * bc * 32;
+    a.div_ow = FastDiv(uint32_t(d.ow));
+    a.div_hw = FastDiv(uint32_t(HW));
+    lds = lds_for(R);
+    blocks = unsigned(d.n) * unsigned(a.tiles_per_img);
+    return true;
+}
+
 template <int G, int OB, bool RS, bool ZW>
 void launch_dw(const DwArgs& a, hipStream_t s)
 {
@@ -1079,6 +1656,30 @@ void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStre
     hipLaunchKernelGGL(conv_i8_table_kernel, dim3(d.oc), dim3(64), 0, stream, d.w, d.oc, K, cstride, kstride, d.bias,
                        d.bias_len, d.zp_x, d.zp_w, rs ? rs->mult : nullptr, rs ? rs->shift : nullptr,
                        rs ? rs->per_channel : 0, rs ? int32_t(rs->rounding == 3) : 0, static_cast<v4i*>(tab));
+}
+
+int64_t conv_i8_wpack_bytes(const ConvI8Desc& d)
+{
+    Halo32Args a{};
+    int bc = 0;
+    size_t lds = 0;
+    unsigned blocks = 0;
+    const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
+                    d.iw == d.ow;
+    if (pw || !conv_i8_fast_supported(d) || !halo32_plan(d, d.zp_w != 0, a, bc, lds, blocks))
+        return 0;
+    return int64_t((d.oc + bc - 1) / bc) * bc * d.kh * d.kw * d.ic;
+}
+
+void conv_i8_wpack(const ConvI8Desc& d, void* wp, hipStream_t stream)
+{
+    const int64_t bytes = conv_i8_wpack_bytes(d);
+    if (bytes <= 0)
+        return;
+    const int bc = d.oc > 64 ? 128 : 64;
+    const int64_t slots = bytes / 16;
+    hipLaunchKernelGGL(conv_i8_wpack_kernel, dim3(unsigned((slots + 255) / 256)), dim3(256), 0, stream, d.w, d.oc,
+                       d.kh * d.kw * d.ic, d.ic, d.kh * d.kw, bc, slots, static_cast<v4u*>(wp));
 }
 
 bool conv_i8_fast_epilogue_ok(const RescaleDev& rs)
@@ -1145,10 +1746,28 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
                     d.iw == d.ow;
 
-    HaloArgs h{};
     int bc = 128, kc = 128;
     size_t lds = 0;
     unsigned blocks = 0;
+    Halo32Args h32{};
+    if (!pw && d.wpack && halo32_plan(d, zw, h32, bc, lds, blocks)) {
+        h32.tab = static_cast<const v4i*>(tab);
+        h32.E = e;
+        const bool k3 = d.kh == 3 && d.kw == 3;
+        if (bc == 128) {
+            if (k3)
+                launch_halo32_epi<128, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+            else
+                launch_halo32_epi<128, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+        } else {
+            if (k3)
+                launch_halo32_epi<64, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+            else
+                launch_halo32_epi<64, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+        }
+        return;
+    }
+    HaloArgs h{};
     if (!pw && halo_plan(d, zw, h, bc, kc, lds, blocks)) {
         h.tab = static_cast<const v4i*>(tab);
         h.E = e;

@@ -236,10 +236,35 @@ StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* b
         if (it != wstore.derived.end())
             return it->second;
     }
-    auto t = make_device_storage(DT_INT32, int64_t(CONV_I8_TABLE_WORDS) * d.oc);
+    auto t = make_device_storage(DT_INT32, conv_i8_table_words(d.oc));
     conv_i8_table(d, rs, t->device_out(), s);
     if (cacheable) {
         hip_check(hipStreamSynchronize(s), "conv_i8 table");
+        std::lock_guard<std::mutex> lk(derived_mu());
+        wstore.derived[key] = t;
+    }
+    return t;
+}
+
+// Packed weights of the stride-1 halo convolution kernel (null when it does
+// not run for `d`), cached on the weight storage when the weight is a graph
+// constant.
+StoragePtr conv_i8_wpack_for(const ConvI8Desc& d, Storage& wstore, bool cacheable, hipStream_t s)
+{
+    const int64_t bytes = conv_i8_wpack_bytes(d);
+    if (bytes <= 0)
+        return nullptr;
+    const std::string key = "conv_i8_wpack:" + std::to_string(bytes);
+    if (cacheable) {
+        std::lock_guard<std::mutex> lk(derived_mu());
+        auto it = wstore.derived.find(key);
+        if (it != wstore.derived.end())
+            return it->second;
+    }
+    auto t = make_device_storage(DT_INT8, bytes);
+    conv_i8_wpack(d, t->device_out(), s);
+    if (cacheable) {
+        hip_check(hipStreamSynchronize(s), "conv_i8 weight pack");
         std::lock_guard<std::mutex> lk(derived_mu());
         wstore.derived[key] = t;
     }
@@ -741,7 +766,8 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         const void* x = input->data->device_in();
         const void* w = weight->data->device_in();
         // Weight and bias are graph constants: derived data may be cached.
-        const bool wb_const = st.const_defs.count(op.inputs[1]) && st.const_defs.count(op.inputs[2]);
+        const bool w_const = st.const_defs.count(op.inputs[1]) != 0;
+        const bool wb_const = w_const && st.const_defs.count(op.inputs[2]);
         ConvI8Desc fd;
         bool fast = false;
         if (mfma_int || dw_int) {
@@ -831,11 +857,14 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         }
         // Keep the operands alive for a later recomputation of a fused-away
         // int32 output.
-        auto launch = [gd, dd, mfma_int, fast, fd, wb_const, x, w, input, weight, bias, wsum_keep](
+        auto launch = [gd, dd, mfma_int, fast, fd, w_const, wb_const, x, w, input, weight, bias, wsum_keep](
                           void* out, const RescaleDev* rs, bool rs_const, uint32_t* err, hipStream_t s) {
             if (fast && (!rs || conv_i8_fast_epilogue_ok(*rs))) {
                 auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), rs, wb_const && (!rs || rs_const), s);
-                conv_i8_fast(fd, tab->device_in(), rs, out, err, s);
+                auto wp = conv_i8_wpack_for(fd, *weight->data, w_const, s);
+                ConvI8Desc f = fd;
+                f.wpack = wp ? static_cast<const int8_t*>(wp->device_in()) : nullptr;
+                conv_i8_fast(f, tab->device_in(), rs, out, err, s);
                 return;
             }
             if (fast && !mfma_int && !depthwise_i8_supported(fd.kh, fd.kw, fd.ic)) {
