@@ -784,9 +784,11 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
         for (int g = 0; g < 4; g++) {
             __builtin_amdgcn_sched_barrier(0);
             v4i t0[4], t1[4];
+            int32_t hi[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 t0[i] = s_tab[2 * (cl + 4 * g + i)];
+                hi[i] = ~t0[i].z;
                 if constexpr (RS)
                     t1[i] = s_tab[2 * (cl + 4 * g + i) + 1];
             }
@@ -801,7 +803,8 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
                         // Same arithmetic as epilogue(): range REQUIRE of
                         // apply_scale_32, 64-bit scale with the per-sign
                         // rounding constant, output zero point and clamp.
-                        bad_bits |= uint32_t(med3(x, t0[i].z, ~t0[i].z)) ^ uint32_t(x);
+                        bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(x, t0[i].z, hi[i])),
+                                                               uint32_t(x), 0xf6);  // bad | (med3 ^ x)
                         const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                         const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                         const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
@@ -811,11 +814,14 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
                     }
                 }
                 if constexpr (OB == 1) {
-                    res[b][g] = (uint32_t(v[0]) & 0xFF) | ((uint32_t(v[1]) & 0xFF) << 8) |
-                                ((uint32_t(v[2]) & 0xFF) << 16) | (uint32_t(v[3]) << 24);
+                    // Low bytes of v0..v3 (v_perm_b32: selector bytes 0-3
+                    // pick the second operand, 4-7 the first, 0x0c zero).
+                    const uint32_t p01 = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x0c0c0400u);
+                    const uint32_t p23 = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x0c0c0400u);
+                    res[b][g] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
                 } else if constexpr (OB == 2) {
-                    res[b][2 * g] = (uint32_t(v[0]) & 0xFFFF) | (uint32_t(v[1]) << 16);
-                    res[b][2 * g + 1] = (uint32_t(v[2]) & 0xFFFF) | (uint32_t(v[3]) << 16);
+                    res[b][2 * g] = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u);
+                    res[b][2 * g + 1] = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; i++)
