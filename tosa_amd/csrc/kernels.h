@@ -35,6 +35,7 @@ struct RescaleDev {
     int32_t has_clamp = 0;
     int64_t clamp_lo = 0, clamp_hi = 0;
     int32_t out_bytes = 1;          // 1, 2 or 4
+    int32_t max_shift = 62;         // largest shift over the channels (host-checked)
 };
 
 // Epilogue of a GEMM-shaped operator.
@@ -100,7 +101,9 @@ struct ConvI8Desc {
 // x (and w for CONV2D).
 bool conv_i8_fast_supported(const ConvI8Desc& d);
 // RESCALEs the fused epilogue handles: scale32 with SINGLE or DOUBLE
-// rounding, signed input with zero point 0 (the only legal one for int32).
+// rounding, signed input with zero point 0 (the only legal one for int32),
+// and an output zero point the table can fold into its rounding constants
+// (|zp| 2^max_shift <= 2^60).
 bool conv_i8_fast_epilogue_ok(const RescaleDev& rs);
 // Per-channel epilogue table (8 int32 per output channel, then 4 int32 of
 // the input zero point's byte, then one int32 per channel) built on the

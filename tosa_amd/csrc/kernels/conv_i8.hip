@@ -48,7 +48,6 @@ struct EpiArgs {
     uint8_t* out;            // NHWC [pixels][N]
     int32_t N;               // output channels
     int32_t zp_w;            // weight zero point (per-pixel correction)
-    int32_t out_zp;          // RESCALE output zero point, |out_zp| < 2^30
     int32_t clo, chi;        // output type range, narrowed to the CLAMP bounds if fused
     uint32_t* err;
 };
@@ -131,13 +130,14 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
                     const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                     // With the value in range and 0 <= multiplier < 2^31 the
                     // scaled result always fits int32 (|r| <= 2^30 + 1), so
-                    // apply_scale_32's result REQUIRE cannot fail, and with
-                    // |output zp| < 2^30 neither can RESCALE's int32 check.
+                    // apply_scale_32's result REQUIRE cannot fail; rp and rn
+                    // carry the output zero point (|zp| <= 2^16), so r is
+                    // already RESCALE's r + zp, which fits int32 as well.
                     const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
                     // Output range and CLAMP in one step: the CLAMP bounds lie
                     // inside the output type's range, so clamping to the
                     // type and then to [clo, chi] is clamping to [clo, chi].
-                    v[i] = med3(r + E.out_zp, E.clo, E.chi);
+                    v[i] = med3(r, E.clo, E.chi);
                 } else {
                     v[i] = x;
                 }
@@ -776,6 +776,19 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
         if constexpr (ZW)
             zwx[b] = int32_t(uint32_t(E.zp_w) * uint32_t(s_rowsum[p]));
     }
+    // Table entries of the lane's channels, one group of 4 at a time, read
+    // a group ahead of the arithmetic that uses them.
+    auto ld_tab = [&](int grp, v4i(&t0)[4], v4i(&t1)[4]) {
+        const int cl = 32 * (grp >> 2) + 16 * h + 4 * (grp & 3);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            t0[i] = s_tab[2 * (cl + i)];
+            if constexpr (RS)
+                t1[i] = s_tab[2 * (cl + i) + 1];
+        }
+    };
+    v4i tn0[4], tn1[4];
+    ld_tab(0, tn0, tn1);
 #pragma unroll
     for (int a = 0; a < TA; a++) {
         const int cl = 32 * a + 16 * h;  // tile channel of element 0
@@ -787,14 +800,14 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
             int32_t hi[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                t0[i] = s_tab[2 * (cl + 4 * g + i)];
+                t0[i] = tn0[i];
+                t1[i] = tn1[i];
                 hi[i] = ~t0[i].z;
-                if constexpr (RS)
-                    t1[i] = s_tab[2 * (cl + 4 * g + i) + 1];
             }
+            if (4 * a + g + 1 < 4 * TA)
+                ld_tab(4 * a + g + 1, tn0, tn1);
 #pragma unroll
             for (int b = 0; b < TB; b++) {
-                __builtin_amdgcn_sched_barrier(0);
                 int32_t v[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -808,7 +821,7 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
                         const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                         const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                         const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
-                        v[i] = med3(r + E.out_zp, E.clo, E.chi);
+                        v[i] = med3(r, E.clo, E.chi);  // output zero point folded into rp, rn
                     } else {
                         v[i] = x;
                     }
@@ -894,8 +907,12 @@ __global__ void __launch_bounds__(BC * 4, 2) conv_i8_halo32_kernel(Halo32Args A)
     const int cw = 64 * (wave >> 2);  // first channel of the wave (tile-relative)
     const int l32 = lane & 31;
     const int h = lane >> 5;
-    const int img = blockIdx.x / A.tiles_per_img;
-    const int oy0 = (blockIdx.x - img * A.tiles_per_img) * A.R;
+    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2);
+    // when their count allows, tile t of XCD x is workgroup x + 8 t, so that
+    // neighbouring row tiles, which share halo rows, meet in one L2.
+    const int tile = (gridDim.x & 7) == 0 ? (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int img = tile / A.tiles_per_img;
+    const int oy0 = (tile - img * A.tiles_per_img) * A.R;
     const int rows = A.OH - oy0 < A.R ? A.OH - oy0 : A.R;
     const int npix = rows * A.OW;
     const int n0 = blockIdx.y * BC;
@@ -1254,7 +1271,7 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
                     const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                     const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                     const int32_t r = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
-                    v[i] = med3(r + A.E.out_zp, A.E.clo, A.E.chi);
+                    v[i] = med3(r, A.E.clo, A.E.chi);
                 } else {
                     v[i] = xv;
                 }
@@ -1278,7 +1295,8 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
 //   tab[2c]   = {bias + K zx zw - zx sum_k w[c][k] (mod 2^32), multiplier,
 //                -2^min(shift - 1, 31), shift}
 //   tab[2c+1] = {rounding constant for values >= 0 (int64, lo/hi),
-//                rounding constant for values < 0 (int64, lo/hi)}
+//                rounding constant for values < 0 (int64, lo/hi)},
+//                both plus out_zp 2^shift
 // then, after the N channels, 16 bytes of the input zero point and the N
 // additive constants (tab[2c].x) as a dense array. The
 // rounding constants are apply_scale_32's 2^(s-1), plus or minus 2^30 under
@@ -1286,7 +1304,7 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
 __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int32_t cstride, int32_t kstride,
                                      const int32_t* bias, int32_t bias_len, int32_t zx, int32_t zw,
                                      const int32_t* mult, const int32_t* shift, int32_t per_channel, int32_t dbl,
-                                     v4i* tab)
+                                     int32_t out_zp, v4i* tab)
 {
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
@@ -1312,7 +1330,11 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
     }
     const int64_t half = int64_t(1) << (sh - 1);
     const int64_t d = (dbl && sh > 31) ? (int64_t(1) << 30) : 0;
-    const int64_t rp = half + d, rn = half - d;
+    // The output zero point rides in the rounding constants: (P + R) >> s
+    // + zp == (P + R + zp 2^s) >> s, and the host admits only zero points
+    // with |zp| 2^s <= 2^60, so P + R + zp 2^s stays inside int64.
+    const int64_t zps = int64_t(out_zp) * (int64_t(1) << sh);
+    const int64_t rp = half + d + zps, rn = half - d + zps;
     // Range bound of apply_scale_32's REQUIRE: values in [lo, ~lo] with
     // lo = -2^min(s - 1, 31).
     const int32_t lo = sh - 1 < 31 ? -(int32_t(1) << (sh - 1)) : INT32_MIN;
@@ -1661,7 +1683,8 @@ void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStre
     const int32_t cstride = d.depthwise ? 1 : K, kstride = d.depthwise ? d.ic : 1;
     hipLaunchKernelGGL(conv_i8_table_kernel, dim3(d.oc), dim3(64), 0, stream, d.w, d.oc, K, cstride, kstride, d.bias,
                        d.bias_len, d.zp_x, d.zp_w, rs ? rs->mult : nullptr, rs ? rs->shift : nullptr,
-                       rs ? rs->per_channel : 0, rs ? int32_t(rs->rounding == 3) : 0, static_cast<v4i*>(tab));
+                       rs ? rs->per_channel : 0, rs ? int32_t(rs->rounding == 3) : 0,
+                       rs ? int32_t(rs->out_zp) : 0, static_cast<v4i*>(tab));
 }
 
 int64_t conv_i8_wpack_bytes(const ConvI8Desc& d)
@@ -1690,11 +1713,15 @@ void conv_i8_wpack(const ConvI8Desc& d, void* wp, hipStream_t stream)
 
 bool conv_i8_fast_epilogue_ok(const RescaleDev& rs)
 {
-    // |out_zp| < 2^30 keeps r + out_zp inside int32 (|r| <= 2^30 + 1); every
-    // legal zero point (int8, uint8, uint16, or 0 for int32) satisfies it.
+    // The table folds the output zero point into the rounding constants,
+    // exact while |zp| 2^max_shift <= 2^60 keeps the 64-bit sum in range;
+    // every legal zero point (int8, uint8, uint16, or 0 for int32) with a
+    // shift up to 45 qualifies. The sum r + zp then fits int32 (|r| <=
+    // 2^30 + 1), so RESCALE's int32 check cannot fail.
+    const int64_t zp = rs.out_zp < 0 ? -rs.out_zp : rs.out_zp;
+    const bool fold = zp == 0 || (rs.max_shift >= 2 && rs.max_shift <= 60 && zp <= (int64_t(1) << (60 - rs.max_shift)));
     return rs.scale32 && (rs.rounding == 1 || rs.rounding == 3) && !rs.in_unsigned && rs.in_zp == 0 &&
-           (rs.out_bytes == 1 || rs.out_bytes == 2 || rs.out_bytes == 4) && rs.out_zp > -(int64_t(1) << 30) &&
-           rs.out_zp < (int64_t(1) << 30);
+           (rs.out_bytes == 1 || rs.out_bytes == 2 || rs.out_bytes == 4) && fold;
 }
 
 void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
@@ -1707,7 +1734,6 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     e.err = err;
     int ob = 4;
     if (rs) {
-        e.out_zp = int32_t(rs->out_zp);
         // CLAMP bounds are values of the output type, so they lie inside
         // [lo, hi] (prepare_clamp_int decodes them in that type).
         e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);

@@ -226,10 +226,10 @@ StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* b
     std::string key;
     if (cacheable) {
         char buf[192];
-        std::snprintf(buf, sizeof buf, "conv_i8_tab:%p:%d:%d:%d:%p:%p:%d:%d", bias_key, d.bias_len, d.zp_x, d.zp_w,
-                      rs ? static_cast<const void*>(rs->mult) : nullptr,
+        std::snprintf(buf, sizeof buf, "conv_i8_tab:%p:%d:%d:%d:%p:%p:%d:%d:%lld", bias_key, d.bias_len, d.zp_x,
+                      d.zp_w, rs ? static_cast<const void*>(rs->mult) : nullptr,
                       rs ? static_cast<const void*>(rs->shift) : nullptr, rs ? rs->per_channel : 0,
-                      rs ? rs->rounding : 0);
+                      rs ? rs->rounding : 0, rs ? static_cast<long long>(rs->out_zp) : 0LL);
         key = buf;
         std::lock_guard<std::mutex> lk(derived_mu());
         auto it = wstore.derived.find(key);
@@ -371,6 +371,9 @@ RescalePrep prepare_rescale(const ExecState& st, const Operator& op, const Tenso
     r.in_unsigned = a.input_unsigned;
     r.in_zp = izp;
     r.out_zp = ozp;
+    r.max_shift = 2;
+    for (int64_t c = 0; c < channels; c++)
+        r.max_shift = std::max<int32_t>(r.max_shift, int32_t(sv[c]));
     if (a.output_unsigned) {
         r.lo = 0;
         r.hi = (int64_t(1) << bit_width(out_t)) - 1;
