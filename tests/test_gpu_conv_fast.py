@@ -232,3 +232,225 @@ def test_fast_conv_halo(case, mode):
         clamp = (-100, 90) if case % 3 == 0 else None
         graph, out = build(x, w, bias, zx, zw, pad, [1, 1], list(dil), rescale=rs, out_dtype=out_dtype, clamp=clamp)
     check(graph, out, {"x": (x, "INT8")})
+
+
+# Convolutions whose input channels the tiled kernels do not take directly
+# (a 3-channel stem, 24-channel 1x1 expansions, strided 1x1): materialised
+# im2col, then the pointwise kernel.
+IM2COL = [
+    # n, h, w, ic, oc, kh, kw, stride, dil
+    (2, 24, 24, 3, 32, 3, 3, (2, 2), (1, 1)),
+    (1, 13, 11, 24, 144, 1, 1, (1, 1), (1, 1)),
+    (2, 9, 10, 8, 40, 3, 3, (1, 1), (1, 1)),
+    (1, 17, 15, 5, 7, 5, 3, (2, 1), (1, 2)),
+    (2, 12, 12, 40, 96, 3, 3, (2, 2), (1, 1)),
+    (1, 10, 14, 12, 130, 2, 2, (1, 1), (2, 1)),
+    (3, 8, 8, 32, 24, 1, 1, (2, 2), (1, 1)),
+    (1, 30, 7, 1, 16, 7, 1, (1, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(IM2COL)))
+@pytest.mark.parametrize("mode", ["i32", "rescale_i8", "rescale_i8_zw"])
+def test_im2col_conv(case, mode):
+    n, h, w_, ic, oc, kh, kw, stride, dil = IM2COL[case]
+    rng = np.random.default_rng(8000 + 10 * case + len(mode))
+    pad = [int(v) for v in rng.integers(0, 2, size=4)]
+    for d, (i, k) in enumerate(((h, kh), (w_, kw))):
+        full = i - 1 + pad[2 * d] + pad[2 * d + 1] - (k - 1) * dil[d]
+        if full < 0:
+            pad[2 * d + 1] += -full
+            full = 0
+        pad[2 * d + 1] += (-full) % stride[d]
+    x = rng.integers(-128, 128, size=(n, h, w_, ic)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(oc, kh, kw, ic)).astype(np.int8)
+    bias = (rng.integers(2 ** 31 - 2 ** 20, 2 ** 31, size=oc) * rng.choice([-1, 1], size=oc)).astype(np.int32)
+    zx = int(rng.integers(-128, 128))
+    zw = int(rng.integers(-128, 128)) if mode == "i32" or mode.endswith("zw") else 0
+    if mode == "i32":
+        graph, out = build(x, w, bias, zx, zw, pad, list(stride), list(dil))
+    else:
+        rs = (rng.integers(2 ** 30, 2 ** 31, size=oc), rng.integers(36, 48, size=oc), int(rng.integers(-128, 128)),
+              case % 2 == 0, True)
+        clamp = (-60, 100) if case % 3 == 0 else None
+        graph, out = build(x, w, bias, zx, zw, pad, list(stride), list(dil), rescale=rs, clamp=clamp)
+    check(graph, out, {"x": (x, "INT8")})
+
+
+def matmul_graph(a, b, azp, bzp, b_const, rescale=None, clamp=None):
+    batch, h, c = a.shape
+    w = b.shape[2]
+    g = GraphBuilder()
+    g.input("a", a.shape, "INT8")
+    if b_const:
+        g.const("b", b, "INT8")
+    else:
+        g.input("b", b.shape, "INT8")
+    g.const("az", np.array([azp]), "INT8")
+    g.const("bz", np.array([bzp]), "INT8")
+    g.tensor("acc", [batch, h, w], "INT32")
+    g.op("MATMUL", ["a", "b", "az", "bz"], ["acc"])
+    out = "acc"
+    if rescale is not None:
+        mult, shift, ozp, dbl, pc = rescale
+        g.const("m", np.asarray(mult, np.int32), "INT32")
+        g.const("s", np.asarray(shift, np.int8), "INT8")
+        g.const("iz", np.array([0]), "INT32")
+        g.const("oz", np.array([ozp]), "INT8")
+        g.tensor("q", [batch, h, w], "INT8")
+        g.op("RESCALE", ["acc", "m", "s", "iz", "oz"], ["q"], scale32=1,
+             rounding_mode="DOUBLE_ROUND" if dbl else "SINGLE_ROUND", per_channel=int(pc))
+        out = "q"
+        if clamp is not None:
+            g.tensor("c", [batch, h, w], "INT8")
+            lo = int(clamp[0]).to_bytes(1, "little", signed=True) + bytes(7)
+            hi = int(clamp[1]).to_bytes(1, "little", signed=True) + bytes(7)
+            g.op("CLAMP", ["q"], ["c"], min_val=lo, max_val=hi)
+            out = "c"
+    return g.build([out]), out
+
+
+# Batched int8 MATMUL with C a multiple of 16: B transposed on the device,
+# then the pointwise kernel with one grid slice per batch.
+MATMUL = [
+    # batch, h, c, w
+    (2, 64, 1280, 1000),
+    (3, 100, 16, 48),
+    (1, 33, 48, 100),
+    (4, 129, 256, 130),
+    (2, 7, 32, 1),
+    (8, 64, 64, 64),
+    (1, 200, 1024, 16),
+]
+
+
+@pytest.mark.parametrize("case", range(len(MATMUL)))
+@pytest.mark.parametrize("mode", ["i32_input_b", "i32_const_b", "rescale_const_b", "rescale_input_b"])
+def test_matmul_tiled(case, mode):
+    batch, h, c, w = MATMUL[case]
+    rng = np.random.default_rng(9000 + 10 * case + len(mode))
+    a = rng.integers(-128, 128, size=(batch, h, c)).astype(np.int8)
+    b = rng.integers(-128, 128, size=(batch, c, w)).astype(np.int8)
+    azp, bzp = int(rng.integers(-128, 128)), int(rng.integers(-128, 128))
+    b_const = "const_b" in mode
+    if mode.startswith("i32"):
+        graph, out = matmul_graph(a, b, azp, bzp, b_const)
+    else:
+        pc = case % 2 == 0
+        cnt = w if pc else 1
+        rs = (rng.integers(2 ** 30, 2 ** 31, size=cnt), rng.integers(38, 50, size=cnt), int(rng.integers(-128, 128)),
+              case % 3 == 0, pc)
+        graph, out = matmul_graph(a, b, azp, bzp, b_const, rescale=rs, clamp=(-50, 120) if case % 2 else None)
+    ins = {"a": (a, "INT8")}
+    if not b_const:
+        ins["b"] = (b, "INT8")
+    ref = oracle_run(graph, ins)[out]
+    for fusion in (True, False):
+        got = run(graph, ins, fusion)[out].numpy()
+        assert np.array_equal(got.reshape(-1).astype(np.int64), ref.vals.reshape(-1).astype(np.int64)), fusion
+
+
+def dw_graph(x, w, bias, zx, zw, pad, stride, rescale):
+    n, ih, iw, c = x.shape
+    kh, kw = w.shape[:2]
+    oh = (ih - 1 + pad[0] + pad[1] - (kh - 1)) // stride[0] + 1
+    ow = (iw - 1 + pad[2] + pad[3] - (kw - 1)) // stride[1] + 1
+    g = GraphBuilder()
+    g.input("x", x.shape, "INT8")
+    g.const("w", w, "INT8")
+    g.const("b", bias, "INT32")
+    g.const("zx", np.array([zx]), "INT8")
+    g.const("zw", np.array([zw]), "INT8")
+    g.tensor("acc", [n, oh, ow, c], "INT32")
+    g.op("DEPTHWISE_CONV2D", ["x", "w", "b", "zx", "zw"], ["acc"], pad=list(pad), stride=list(stride),
+         dilation=[1, 1], acc_type="INT32")
+    mult, shift, ozp = rescale
+    g.const("m", np.asarray(mult, np.int32), "INT32")
+    g.const("s", np.asarray(shift, np.int8), "INT8")
+    g.const("iz", np.array([0]), "INT32")
+    g.const("oz", np.array([ozp]), "INT8")
+    g.tensor("q", [n, oh, ow, c], "INT8")
+    g.op("RESCALE", ["acc", "m", "s", "iz", "oz"], ["q"], scale32=1, rounding_mode="DOUBLE_ROUND", per_channel=1)
+    return g.build(["q"])
+
+
+@pytest.mark.parametrize("c", [16, 32, 48, 96])
+def test_depthwise_range_checked_shifts(c):
+    """Shifts from 16 to 31 on the MFMA depthwise kernel: the value-range
+    REQUIRE is live; small weights keep every value inside it."""
+    rng = np.random.default_rng(400 + c)
+    x = rng.integers(-128, 128, size=(2, 9, 11, c)).astype(np.int8)
+    w = rng.integers(-2, 3, size=(3, 3, c, 1)).astype(np.int8)
+    bias = rng.integers(-1000, 1000, size=c).astype(np.int32)
+    rs = (rng.integers(2 ** 30, 2 ** 31, size=c), rng.integers(16, 32, size=c), 3)
+    graph = dw_graph(x, w, bias, -5, 0, [1, 1, 1, 1], [1, 1], rs)
+    ins = {"x": (x, "INT8")}
+    ref = oracle_run(graph, ins)["q"].vals
+    for fusion in (True, False):
+        got = run(graph, ins, fusion)["q"].numpy()
+        assert np.array_equal(got.reshape(-1).astype(np.int64), ref.reshape(-1).astype(np.int64)), fusion
+
+
+def test_depthwise_range_require_failure():
+    rng = np.random.default_rng(401)
+    x = rng.integers(-128, 128, size=(1, 8, 8, 32)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(3, 3, 32, 1)).astype(np.int8)
+    graph = dw_graph(x, w, np.zeros(32, np.int32), 0, 0, [1, 1, 1, 1], [1, 1],
+                     (np.full(32, 2 ** 30), np.full(32, 6), 0))
+    with pytest.raises(O.OracleError):
+        oracle_run(graph, {"x": (x, "INT8")})
+    with pytest.raises(T.TosaError) as e:
+        run(graph, {"x": (x, "INT8")})
+    assert e.value.kind == "GraphError"
+
+
+# Images of at least 28 x 28 take the LDS-tiled depthwise kernel (every
+# channel of a tile of output rows per workgroup).
+DW_LDS = [
+    # n, h, w, c, kh, kw, stride, dil, pad, zw, shifts
+    (1, 28, 28, 16, 3, 3, (1, 1), (1, 1), (1, 1, 1, 1), 0, (36, 44)),
+    (2, 30, 29, 48, 3, 3, (2, 2), (1, 1), (0, 1, 0, 0), 3, (36, 44)),
+    (1, 32, 40, 64, 3, 3, (1, 1), (2, 2), (2, 2, 2, 2), -2, (36, 44)),
+    (2, 28, 31, 32, 1, 3, (1, 1), (1, 1), (0, 0, 1, 1), 0, (20, 32)),
+    (1, 28, 28, 96, 2, 2, (1, 2), (1, 1), (0, 1, 0, 0), 4, (36, 44)),
+    (1, 56, 56, 144, 3, 3, (2, 2), (1, 1), (0, 1, 0, 1), -1, (36, 44)),
+    (1, 29, 33, 960, 3, 3, (1, 1), (1, 1), (1, 1, 1, 1), 2, (36, 44)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(DW_LDS)))
+def test_depthwise_lds_tiles(case):
+    n, h, w_, c, kh, kw, stride, dil, pad, zw, (slo, shi) = DW_LDS[case]
+    rng = np.random.default_rng(500 + case)
+    oh = (h - 1 + pad[0] + pad[1] - (kh - 1) * dil[0]) // stride[0] + 1
+    ow = (w_ - 1 + pad[2] + pad[3] - (kw - 1) * dil[1]) // stride[1] + 1
+    assert (h - 1 + pad[0] + pad[1] - (kh - 1) * dil[0]) % stride[0] == 0
+    assert (w_ - 1 + pad[2] + pad[3] - (kw - 1) * dil[1]) % stride[1] == 0
+    x = rng.integers(-128, 128, size=(n, h, w_, c)).astype(np.int8)
+    small = slo < 32
+    w = rng.integers(-2, 3, size=(kh, kw, c, 1)).astype(np.int8) if small else \
+        rng.integers(-128, 128, size=(kh, kw, c, 1)).astype(np.int8)
+    bias = rng.integers(-1000, 1000, size=c).astype(np.int32) if small else \
+        rng.integers(-2 ** 20, 2 ** 20, size=c).astype(np.int32)
+    g = GraphBuilder()
+    g.input("x", x.shape, "INT8")
+    g.const("w", w, "INT8")
+    g.const("b", bias, "INT32")
+    g.const("zx", np.array([int(rng.integers(-128, 128))]), "INT8")
+    g.const("zw", np.array([zw]), "INT8")
+    g.tensor("acc", [n, oh, ow, c], "INT32")
+    g.op("DEPTHWISE_CONV2D", ["x", "w", "b", "zx", "zw"], ["acc"], pad=list(pad), stride=list(stride),
+         dilation=list(dil), acc_type="INT32")
+    g.const("m", rng.integers(2 ** 30, 2 ** 31, size=c).astype(np.int32), "INT32")
+    g.const("s", rng.integers(slo, shi, size=c).astype(np.int8), "INT8")
+    g.const("iz", np.array([0]), "INT32")
+    g.const("oz", np.array([int(rng.integers(-20, 20))]), "INT8")
+    g.tensor("q", [n, oh, ow, c], "INT8")
+    g.op("RESCALE", ["acc", "m", "s", "iz", "oz"], ["q"], scale32=1, rounding_mode="DOUBLE_ROUND", per_channel=1)
+    for out in ("q", "acc"):
+        graph = g.build([out])
+        ins = {"x": (x, "INT8")}
+        ref = oracle_run(graph, ins)[out].vals
+        for fusion in (True, False):
+            got = run(graph, ins, fusion)[out].numpy()
+            assert np.array_equal(got.reshape(-1).astype(np.int64), ref.reshape(-1).astype(np.int64)), (out, fusion)

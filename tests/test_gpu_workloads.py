@@ -354,6 +354,72 @@ def test_residual_fusion_matches_unfused():
         assert same_int(run(graph, ins, fusion)["y"].numpy(), ref), fusion
 
 
+# (channels, input shifts, output shift range, double rounding of a/b/out,
+# per-channel a/b/out): shifts >= 9 on the int8 inputs take the residual
+# kernel whose REQUIREs are settled on the host; a shift of 8 falls back to
+# the per-element kernel.
+RESIDUAL = [
+    (24, 20, (34, 40), (False, False, True), (True, False, True)),
+    (32, 9, (44, 50), (True, True, True), (True, True, False)),
+    (96, 12, (42, 47), (False, True, False), (False, True, True)),
+    (160, 30, (24, 30), (True, False, True), (True, True, True)),
+    (8, 8, (46, 50), (False, False, False), (True, True, True)),
+    (1024, 16, (38, 43), (True, True, True), (True, True, True)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(RESIDUAL)))
+def test_residual_paths(case):
+    c, sin, (slo, shi), dbl, pc = RESIDUAL[case]
+    rng = np.random.default_rng(300 + case)
+    shape = (3, 5, 7, c)
+    a = rng.integers(-128, 128, size=shape).astype(np.int8)
+    b = rng.integers(-128, 128, size=shape).astype(np.int8)
+    g = GraphBuilder()
+    g.input("a", shape, "INT8")
+    g.input("b", shape, "INT8")
+    ca, cb, co = (c if pc[0] else 1), (c if pc[1] else 1), (c if pc[2] else 1)
+    # A shift of 8 admits |a - za| < 128 only: zero input zero points there.
+    za, zb = (int(v) for v in rng.integers(-128, 128, 2)) if sin >= 9 else (0, 0)
+    W._rescale(g, "a", g.tensor("ra", shape, "INT32"), c, rng.integers(2 ** 30, 2 ** 31, ca), [sin] * ca, "INT8",
+               "INT32", za, 0, dbl[0], pc[0], "x1")
+    W._rescale(g, "b", g.tensor("rb", shape, "INT32"), c, rng.integers(2 ** 30, 2 ** 31, cb),
+               rng.integers(sin, sin + 3, cb), "INT8", "INT32", zb, 0, dbl[1], pc[1], "x2")
+    g.tensor("s", shape, "INT32")
+    g.op("ADD", ["ra", "rb"], ["s"])
+    W._rescale(g, "s", g.tensor("y", shape, "INT8"), c, rng.integers(2 ** 30, 2 ** 31, co),
+               rng.integers(slo, shi, co), "INT32", "INT8", 0, int(rng.integers(-128, 128)),
+               dbl[2], pc[2], "x3")
+    graph = g.build(["y"])
+    ins = {"a": (a, "INT8"), "b": (b, "INT8")}
+    ref = oracle_run(graph, ins)["y"].vals
+    for fusion in (True, False):
+        assert same_int(run(graph, ins, fusion)["y"].numpy(), ref), fusion
+
+
+def test_residual_range_require():
+    """An output shift below 32 whose sums fall outside [-2^(s-1), 2^(s-1))
+    is apply_scale_32's REQUIRE failure, reported as GraphError."""
+    shape = (2, 4, 4, 16)
+    a = np.full(shape, 100, np.int8)
+    g = GraphBuilder()
+    g.input("a", shape, "INT8")
+    g.input("b", shape, "INT8")
+    W._rescale(g, "a", g.tensor("ra", shape, "INT32"), 16, [2 ** 30], [10], "INT8", "INT32", 0, 0, False, False, "x1")
+    W._rescale(g, "b", g.tensor("rb", shape, "INT32"), 16, [2 ** 30], [10], "INT8", "INT32", 0, 0, False, False, "x2")
+    g.tensor("s", shape, "INT32")
+    g.op("ADD", ["ra", "rb"], ["s"])
+    W._rescale(g, "s", g.tensor("y", shape, "INT8"), 16, [2 ** 30], [6], "INT32", "INT8", 0, 0, False, False, "x3")
+    graph = g.build(["y"])
+    ins = {"a": (a, "INT8"), "b": (a, "INT8")}
+    with pytest.raises(O.OracleError):
+        oracle_run(graph, ins)
+    for fusion in (True, False):
+        with pytest.raises(T.TosaError) as e:
+            run(graph, ins, fusion)
+        assert e.value.kind == "GraphError"
+
+
 @pytest.mark.parametrize("c", [3, 8, 1280])
 def test_avg_pool_int8_paths(c):
     rng = np.random.default_rng(c)

@@ -36,6 +36,7 @@ struct RescaleDev {
     int64_t clamp_lo = 0, clamp_hi = 0;
     int32_t out_bytes = 1;          // 1, 2 or 4
     int32_t max_shift = 62;         // largest shift over the channels (host-checked)
+    int32_t min_shift = 2;          // smallest shift over the channels
 };
 
 // Epilogue of a GEMM-shaped operator.
@@ -94,6 +95,11 @@ struct ConvI8Desc {
     // Weights packed by conv_i8_wpack (when conv_i8_wpack_bytes > 0); the
     // stride-1 halo kernel runs only with them.
     const int8_t* wpack = nullptr;
+    // Independent pointwise problems (1x1 stride-1 unpadded CONV2D only):
+    // x [batch][n oh ow][ic], w [batch][oc][ic], out [batch][n oh ow][oc] and
+    // the table [batch][conv_i8_table_stride(oc)]. A batched MATMUL runs as
+    // this with B transposed to rows of C bytes.
+    int32_t batch = 1;
 };
 // Geometry and alignment the kernels handle: CONV2D 1x1 stride-1 unpadded
 // with ic % 16 == 0, any other CONV2D geometry with ic % 64 == 0;
@@ -111,11 +117,33 @@ bool conv_i8_fast_epilogue_ok(const RescaleDev& rs);
 // multiplier and shift.
 constexpr int CONV_I8_TABLE_WORDS = 8;
 inline int64_t conv_i8_table_words(int32_t oc) { return int64_t(CONV_I8_TABLE_WORDS + 1) * oc + 4; }
+// int32 words between the tables of consecutive batches (64-byte aligned).
+inline int64_t conv_i8_table_stride(int32_t oc) { return (conv_i8_table_words(oc) + 15) / 16 * 16; }
+// Words of a table for all of d's batches.
+inline int64_t conv_i8_table_words(int32_t oc, int32_t batch)
+{
+    return int64_t(batch - 1) * conv_i8_table_stride(oc) + conv_i8_table_words(oc);
+}
 void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStream_t stream);
 // Bytes of the packed weight layout of the stride-1 halo kernel for `d`, 0
 // when that kernel does not run for `d`; conv_i8_wpack writes it from d.w.
 int64_t conv_i8_wpack_bytes(const ConvI8Desc& d);
 void conv_i8_wpack(const ConvI8Desc& d, void* wp, hipStream_t stream);
+// Convolutions that conv_i8_fast_supported rejects only for their channel
+// alignment or geometry run as a pointwise GEMM over a materialised im2col:
+// X~ [n oh ow][Kp] (Kp = K rounded up to 16; padding taps hold the input
+// zero point, columns past K hold 0) and the weights as [oc][Kp] rows
+// (zero-filled). The table is still built from the original descriptor.
+int32_t conv_i8_im2col_kp(const ConvI8Desc& d);
+void conv_i8_im2col(const ConvI8Desc& d, int8_t* xcol, hipStream_t stream);
+void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t* out, hipStream_t stream);
+// MATMUL right operand [batch][c][w] -> [batch][w][c] (c % 16 == 0).
+void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream);
+// DEPTHWISE_CONV2D (multiplier 1, ic % 16 == 0, at most 12 taps) over
+// LDS-staged input tiles (dw_i8.hip); false when the shape does not fit its
+// LDS budget. Same table and epilogue contract as conv_i8_fast.
+bool depthwise_i8_lds(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                      hipStream_t stream);
 // The convolution; `rs` selects the fused RESCALE (+CLAMP) epilogue with the
 // table built for the same `rs`, else the int32 output (conv + bias).
 void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,

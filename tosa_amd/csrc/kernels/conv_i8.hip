@@ -28,6 +28,8 @@
 // the epilogue stores as one vector.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "kcommon.h"
 
 namespace tosa {
@@ -50,7 +52,11 @@ struct EpiArgs {
     int32_t zp_w;            // weight zero point (per-pixel correction)
     int32_t clo, chi;        // output type range, narrowed to the CLAMP bounds if fused
     uint32_t* err;
+    // Some channel's shift is below 32, so apply_scale_32's value-range
+    // REQUIRE can fail and is checked (with every shift >= 32 it cannot).
+    int32_t range;
 };
+
 
 struct ConvI8Args {
     const int8_t* x;
@@ -61,6 +67,10 @@ struct ConvI8Args {
     FastDiv div_ohow, div_ow;
     int32_t zp_x;
     EpiArgs E;
+    // Pointwise batches (blockIdx.z): strides of x, w and out in bytes and
+    // of the table in 16-byte entries.
+    int64_t bsx, bsw, bso;
+    int32_t bst, batch;
 };
 
 // Median of three (v_med3_i32): clamp of v to [lo, hi] when lo <= hi.
@@ -90,42 +100,48 @@ __device__ __forceinline__ int swz(int row)
 // consecutive channels starting at tile channel `cl0` of tile pixel
 // wave_p0 + 16 tn + j16; `pixel(p)` maps a tile pixel to its output row
 // (NHWC pixel index) or -1 when the pixel does not exist.
-template <int TM, int TN, int OB, bool RS, bool ZW, typename PixelMap>
+template <int TM, int TN, int OB, bool RS, bool ZW, bool RC, typename PixelMap>
 __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, const int32_t* s_rowsum, int cl0,
                                          int n0, int wave_p0, int j16, const EpiArgs& E, PixelMap pixel)
 {
     constexpr int WORDS = TM * OB;  // 32-bit words of output per lane and pixel
     const int c0 = n0 + cl0;
     uint32_t res[TN][WORDS];
-    bool bad_range = false;
+    // Nonzero when a value fails apply_scale_32's range REQUIRE (one bitwise
+    // op per value on the VALU).
+    uint32_t bad_bits = 0;
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
         // One channel group at a time: keeps the scheduler from hoisting every
         // group's table reads (32 registers each) to the top.
         __builtin_amdgcn_sched_barrier(0);
         v4i t0[4], t1[4];
+        int32_t hi[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             t0[i] = s_tab[2 * (cl0 + 4 * tm + i)];
             if constexpr (RS)
                 t1[i] = s_tab[2 * (cl0 + 4 * tm + i) + 1];
+            hi[i] = ~t0[i].z;
         }
 #pragma unroll
         for (int tn = 0; tn < TN; tn++) {
             // Four outputs at a time (bounds the 64-bit temporaries in flight).
             __builtin_amdgcn_sched_barrier(0);
-            int32_t zwx = 0;
+            uint32_t nzwx = 0;  // -zw sum_k x~ of the pixel
             if constexpr (ZW)
-                zwx = int32_t(uint32_t(E.zp_w) * uint32_t(s_rowsum[wave_p0 + 16 * tn + j16]));
+                nzwx = uint32_t(-E.zp_w) * uint32_t(s_rowsum[wave_p0 + 16 * tn + j16]);
             int32_t v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int32_t x = int32_t(uint32_t(acc[tm][tn][i]) + uint32_t(t0[i].x) - uint32_t(zwx));
+                const int32_t x = int32_t(uint32_t(acc[tm][tn][i]) + uint32_t(t0[i].x) + nzwx);
                 if constexpr (RS) {
                     // apply_scale_32: the value must lie in [-2^(s-1), 2^(s-1)),
                     // a condition on int32 values only for shifts below 32
                     // (t0.z = -2^min(s - 1, 31), ~t0.z = 2^min(s - 1, 31) - 1).
-                    bad_range |= med3(x, t0[i].z, ~t0[i].z) != x;
+                    if constexpr (RC)
+                        bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(x, t0[i].z, hi[i])),
+                                                               uint32_t(x), 0xf6);  // bad | (med3 ^ x)
                     const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                     const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                     // With the value in range and 0 <= multiplier < 2^31 the
@@ -143,8 +159,7 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
                 }
             }
             if constexpr (OB == 1) {
-                res[tn][tm] = (uint32_t(v[0]) & 0xFF) | ((uint32_t(v[1]) & 0xFF) << 8) |
-                              ((uint32_t(v[2]) & 0xFF) << 16) | (uint32_t(v[3]) << 24);
+                res[tn][tm] = pack4_u8(v[0], v[1], v[2], v[3]);
             } else if constexpr (OB == 2) {
                 res[tn][2 * tm] = (uint32_t(v[0]) & 0xFFFF) | (uint32_t(v[1]) << 16);
                 res[tn][2 * tm + 1] = (uint32_t(v[2]) & 0xFFFF) | (uint32_t(v[3]) << 16);
@@ -159,6 +174,8 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
 #pragma unroll
             for (int w = 0; w < OB; w++)
                 asm volatile("" : "+v"(res[tn][tm * OB + w]));
+            if constexpr (RS && RC)
+                asm volatile("" : "+v"(bad_bits));
         }
     }
 
@@ -170,7 +187,7 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
         const int64_t o = int64_t(m) * E.N + c0;
         uint8_t* dst = E.out + o * OB;
         constexpr int VB = 4 * WORDS;  // bytes this lane holds for the pixel
-        if (c0 + 4 * TM <= E.N && ((o * OB) % (VB < 16 ? VB : 16)) == 0) {
+        if (c0 + 4 * TM <= E.N && (reinterpret_cast<uintptr_t>(dst) % (VB < 16 ? VB : 16)) == 0) {
             if constexpr (WORDS % 4 == 0) {
 #pragma unroll
                 for (int w = 0; w < WORDS; w += 4)
@@ -197,7 +214,7 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
             }
         }
     }
-    if (bad_range)
+    if (bad_bits)
         atomicOr(E.err, DERR_SCALE_RANGE);
 }
 
@@ -206,8 +223,16 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
 // multiple of 16). OB: output bytes (1, 2, 4). RS: RESCALE epilogue (else
 // int32 + bias). ZW: weight zero point is nonzero.
 template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW>
-__global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
+__global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args Ain)
 {
+    ConvI8Args A = Ain;
+    if constexpr (PW) {
+        const int z = blockIdx.z;
+        A.x += z * A.bsx;
+        A.w += z * A.bsw;
+        A.tab += z * A.bst;
+        A.E.out += z * A.bso;
+    }
     constexpr int TM = BC / WC / 16;
     constexpr int TN = BP / WP / 16;
     constexpr int CPR = KC / 16;              // 16-byte chunks per LDS row
@@ -352,6 +377,10 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
 
     const int j16 = lane & 15;
     const int grp = lane >> 4;
+    // A wave whose channels all lie past N (the last channel tile of a
+    // layer whose channel count is not a multiple of the tile) only helps
+    // to stage: no MFMAs, no epilogue.
+    const bool wave_live = n0 + wave_c0 < A.N;
     for (int s = 0; s < nst; s++) {
         const int buf = s & 1;
         if (s + 1 < nst) {
@@ -361,7 +390,7 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
         const uint8_t* a = sA + buf * BC * KC;
         const uint8_t* b = sB + buf * BP * KC;
 #pragma unroll
-        for (int ks = 0; ks < KC / 64; ks++) {
+        for (int ks = 0; ks < (wave_live ? KC / 64 : 0); ks++) {
             const int c = ks * 4 + grp;
             v4i af[TM], bf[TN];
 #pragma unroll
@@ -400,8 +429,15 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args A)
     }
 
     // ---- epilogue ----------------------------------------------------------
-    epilogue<TM, TN, OB, RS, ZW>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
-                                 [&](int p) { return m0 + p < A.M ? m0 + p : -1; });
+    if (wave_live) {
+        auto pixel = [&](int p) { return m0 + p < A.M ? m0 + p : -1; };
+        if (!RS || A.E.range)
+            epilogue<TM, TN, OB, RS, ZW, true>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
+                                               pixel);
+        else
+            epilogue<TM, TN, OB, RS, ZW, false>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
+                                                pixel);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -680,8 +716,12 @@ __global__ void __launch_bounds__(HALO_NT, 2) conv_i8_halo_kernel(HaloArgs A)
     }
 
     const int m0 = (img * A.OH + oy0) * A.OW;
-    epilogue<TM, TN, OB, RS, ZW>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
-                                 [&](int p) { return p < npix ? m0 + p : -1; });
+    auto pixel = [&](int p) { return p < npix ? m0 + p : -1; };
+    if (!RS || A.E.range)
+        epilogue<TM, TN, OB, RS, ZW, true>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E, pixel);
+    else
+        epilogue<TM, TN, OB, RS, ZW, false>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
+                                            pixel);
 }
 
 // ---------------------------------------------------------------------------
@@ -1151,6 +1191,167 @@ __global__ void conv_i8_wpack_kernel(const int8_t* w, int32_t N, int32_t K, int3
 }
 
 // ---------------------------------------------------------------------------
+// Materialised im2col for the convolutions the tiled kernels do not take
+// directly (input channels that are not a multiple of the stage width, e.g.
+// a 3-channel stem): X~[m][k], k = (ky KW + kx) IC + ic < K, holds the input
+// byte at the tap (the input zero point outside the input, which the
+// zero-point fold turns into the reference's skipped tap), and K <= k < Kp
+// holds 0 (a zero weight column multiplies it). The pointwise kernel then
+// runs over X~ with the weights padded to [OC][Kp]. One thread per 16-byte
+// chunk (blockIdx.y) of one row (pixel); the tap of each byte is uniform.
+// ---------------------------------------------------------------------------
+struct Im2colArgs {
+    const int8_t* x;
+    int8_t* out;
+    int32_t M, K, Kp, IC;
+    int32_t ih, iw, kw, ohow, ow, pt, pl, sy, sx, dy, dx;
+    FastDiv div_ohow, div_ow;
+    int32_t zp_x;
+};
+
+__global__ void __launch_bounds__(256) conv_i8_im2col_kernel(Im2colArgs A)
+{
+    const int m = blockIdx.x * 256 + threadIdx.x;
+    if (m >= A.M)
+        return;
+    const int k0 = blockIdx.y * 16;
+    const int b = fdiv(m, A.div_ohow);
+    const int rem = m - b * A.ohow;
+    const int oy = fdiv(rem, A.div_ow);
+    const int ox = rem - oy * A.ow;
+    const int iy0 = oy * A.sy - A.pt, ix0 = ox * A.sx - A.pl;
+    const int8_t* xb = A.x + int64_t(b) * A.ih * A.iw * A.IC;
+    uint32_t wv[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int k = k0 + j;
+        uint32_t v = 0;
+        if (k < A.K) {
+            const int t = k / A.IC, ic = k - t * A.IC;
+            const int ky = t / A.kw, kx = t - ky * A.kw;
+            const int iy = iy0 + ky * A.dy, ix = ix0 + kx * A.dx;
+            const bool ok = unsigned(iy) < unsigned(A.ih) && unsigned(ix) < unsigned(A.iw);
+            v = ok ? uint8_t(xb[(int64_t(iy) * A.iw + ix) * A.IC + ic]) : uint8_t(A.zp_x);
+        }
+        wv[j >> 2] |= v << (8 * (j & 3));
+    }
+    *reinterpret_cast<v4u*>(A.out + int64_t(m) * A.Kp + k0) = v4u{wv[0], wv[1], wv[2], wv[3]};
+}
+
+// The same with the taps of the first IM2COL_TAB columns tabulated on the
+// host (a uniform kernel argument per column: its offset from the pixel's
+// origin, or -1 past K, and its row and column displacement), so a column
+// costs one load and a bounds test. DW4: IC % 4 == 0, four columns of one
+// tap per 32-bit load.
+constexpr int IM2COL_TAB = 128;
+struct Im2colTab {
+    int32_t off[IM2COL_TAB];
+    int16_t dy[IM2COL_TAB], dx[IM2COL_TAB];
+};
+
+template <bool DW4>
+__global__ void __launch_bounds__(256) conv_i8_im2col_tab_kernel(Im2colArgs A, Im2colTab T)
+{
+    const int m = blockIdx.x * 256 + threadIdx.x;
+    if (m >= A.M)
+        return;
+    const int k0 = blockIdx.y * 16;
+    const int b = fdiv(m, A.div_ohow);
+    const int rem = m - b * A.ohow;
+    const int oy = fdiv(rem, A.div_ow);
+    const int ox = rem - oy * A.ow;
+    const int iy0 = oy * A.sy - A.pt, ix0 = ox * A.sx - A.pl;
+    const int8_t* xp = A.x + int64_t(b) * A.ih * A.iw * A.IC + (int64_t(iy0) * A.iw + ix0) * A.IC;
+    const uint32_t zf = uint32_t(uint8_t(A.zp_x)) * 0x01010101u;
+    uint32_t wv[4] = {0, 0, 0, 0};
+    if constexpr (DW4) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int k = k0 + 4 * q;
+            const int o = T.off[k];
+            if (o >= 0) {
+                const int iy = iy0 + T.dy[k], ix = ix0 + T.dx[k];
+                const bool ok = unsigned(iy) < unsigned(A.ih) && unsigned(ix) < unsigned(A.iw);
+                wv[q] = ok ? *reinterpret_cast<const uint32_t*>(xp + o) : zf;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int k = k0 + j;
+            const int o = T.off[k];
+            if (o >= 0) {
+                const int iy = iy0 + T.dy[k], ix = ix0 + T.dx[k];
+                const bool ok = unsigned(iy) < unsigned(A.ih) && unsigned(ix) < unsigned(A.iw);
+                const uint32_t v = ok ? uint8_t(xp[o]) : uint8_t(A.zp_x);
+                wv[j >> 2] |= v << (8 * (j & 3));
+            }
+        }
+    }
+    *reinterpret_cast<v4u*>(A.out + int64_t(m) * A.Kp + k0) = v4u{wv[0], wv[1], wv[2], wv[3]};
+}
+
+// Rows of K bytes copied into rows of Kp >= K bytes, zero-filled.
+__global__ void conv_i8_rowpad_kernel(const int8_t* w, int32_t rows, int32_t K, int32_t Kp, int8_t* out)
+{
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(rows) * Kp)
+        return;
+    const int64_t r = i / Kp;
+    const int k = int(i - r * Kp);
+    out[i] = k < K ? w[r * K + k] : int8_t(0);
+}
+
+// B [batch][C][W] -> [batch][W][C] (the MATMUL right operand as OHWI-style
+// rows of C bytes), 64 x 64 byte tiles through LDS. C % 16 == 0; VEC: W % 16
+// == 0, so the rows of B load as 16-byte vectors.
+template <bool VEC>
+__global__ void __launch_bounds__(256) transpose_b_kernel(const int8_t* b, int32_t C, int32_t W, int8_t* out)
+{
+    __shared__ uint8_t t[64][64 + 4];
+    const int z = blockIdx.z;
+    const int c0 = blockIdx.y * 64, w0 = blockIdx.x * 64;
+    const int8_t* src = b + int64_t(z) * C * W;
+    int8_t* dst = out + int64_t(z) * C * W;
+    const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
+    // load: row c0 + r, columns w0 + 16 q .. + 15
+    {
+        const int c = c0 + r;
+        const int w = w0 + 16 * q;
+        uint32_t v[4] = {0, 0, 0, 0};
+        if (c < C) {
+            if (VEC) {
+                if (w < W) {
+                    const v4u x = *reinterpret_cast<const v4u*>(src + int64_t(c) * W + w);
+                    v[0] = x.x;
+                    v[1] = x.y;
+                    v[2] = x.z;
+                    v[3] = x.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (w + j < W)
+                        v[j >> 2] |= uint32_t(uint8_t(src[int64_t(c) * W + w + j])) << (8 * (j & 3));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *reinterpret_cast<uint32_t*>(&t[r][16 * q + 4 * j]) = v[j];
+    }
+    __syncthreads();
+    // store: output row w0 + r, columns c0 + 16 q .. + 15
+    const int w = w0 + r, c = c0 + 16 * q;
+    if (w >= W || c >= C)
+        return;
+    uint32_t v[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; j++)
+        v[j >> 2] |= uint32_t(t[16 * q + j][r]) << (8 * (j & 3));
+    *reinterpret_cast<v4u*>(dst + int64_t(w) * C + c) = v4u{v[0], v[1], v[2], v[3]};
+}
+
+// ---------------------------------------------------------------------------
 // DEPTHWISE_CONV2D (depth multiplier 1) on MFMA
 // ---------------------------------------------------------------------------
 // For 16 channels c0..c0+15 and 16 output pixels, the depthwise sum
@@ -1179,12 +1380,21 @@ struct DwArgs {
 template <int G, int OB, bool RS, bool ZW>
 __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
 {
-    constexpr int TN = 4;  // 16-pixel tiles per workgroup
+    constexpr int TN = 4;  // 16-pixel tiles per wave
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j16 = lane & 15;
     const int grp = lane >> 4;
-    const int p0 = blockIdx.x * (16 * TN);
+    // Work item of the wave: (64-pixel tile, 16-channel group), channel
+    // groups fastest, so every wave has work whatever the channel count and
+    // the waves of a workgroup read neighbouring channels of the same pixels.
+    const int groups = A.C >> 4;
+    const int item = blockIdx.x * 4 + wave;
+    const int ptile = item / groups;
+    const int cg = item - ptile * groups;
+    const int p0 = ptile * (16 * TN);
+    if (p0 >= A.P)
+        return;
     const uint32_t zf = uint32_t(uint8_t(A.zp_x)) * 0x01010101u;
     const v4u zfill = v4u{zf, zf, zf, zf};
 
@@ -1216,8 +1426,7 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
         tdx[g] = (t - ky * A.KW) * A.dx;
     }
 
-    const int cg = blockIdx.y * 4 + wave;
-    if (cg < (A.C >> 4)) {
+    {
         const int c0 = cg * 16;
         // Block-diagonal A fragments: byte j16 of 16 is w[t][c0 + j16].
         v4i wa[G], wo[G];
@@ -1243,7 +1452,14 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
             if constexpr (RS)
                 t1[i] = A.tab[2 * (c0 + 4 * grp + i) + 1];
         }
-        bool bad_range = false;
+        int32_t hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            hi[i] = ~t0[i].z;
+        uint32_t bad_bits = 0;
+        // RC: some shift is below 32, so the value-range REQUIRE is checked.
+        auto tiles = [&](auto rc) {
+            constexpr bool RC = decltype(rc)::value;
 #pragma unroll
         for (int tn = 0; tn < TN; tn++) {
             v4i acc = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
@@ -1263,11 +1479,14 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
             int32_t v[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                int32_t xv = int32_t(uint32_t(acc[i]) + uint32_t(t0[i].x));
+                uint32_t xu = uint32_t(acc[i]) + uint32_t(t0[i].x);
                 if constexpr (ZW)
-                    xv = int32_t(uint32_t(xv) - uint32_t(A.E.zp_w) * uint32_t(acc1[i]));
+                    xu += uint32_t(-A.E.zp_w) * uint32_t(acc1[i]);
+                const int32_t xv = int32_t(xu);
                 if constexpr (RS) {
-                    bad_range |= med3(xv, t0[i].z, ~t0[i].z) != xv;
+                    if constexpr (RC)
+                        bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(xv, t0[i].z, hi[i])),
+                                                               uint32_t(xv), 0xf6);  // bad | (med3 ^ x)
                     const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
                     const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
                     const int32_t r = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
@@ -1278,15 +1497,21 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
             }
             uint8_t* dst = A.E.out + (int64_t(p0 + 16 * tn + j16) * A.C + c0 + 4 * grp) * OB;
             if constexpr (OB == 1)
-                *reinterpret_cast<uint32_t*>(dst) = (uint32_t(v[0]) & 0xFF) | ((uint32_t(v[1]) & 0xFF) << 8) |
-                                                    ((uint32_t(v[2]) & 0xFF) << 16) | (uint32_t(v[3]) << 24);
+                *reinterpret_cast<uint32_t*>(dst) = pack4_u8(v[0], v[1], v[2], v[3]);
             else if constexpr (OB == 2)
                 *reinterpret_cast<v2u*>(dst) = v2u{(uint32_t(v[0]) & 0xFFFF) | (uint32_t(v[1]) << 16),
                                                    (uint32_t(v[2]) & 0xFFFF) | (uint32_t(v[3]) << 16)};
             else
                 *reinterpret_cast<v4i*>(dst) = v4i{v[0], v[1], v[2], v[3]};
+            if constexpr (RS && RC)
+                asm volatile("" : "+v"(bad_bits));
         }
-        if (bad_range)
+        };
+        if (!RS || A.E.range)
+            tiles(std::true_type{});
+        else
+            tiles(std::false_type{});
+        if (bad_bits)
             atomicOr(A.E.err, DERR_SCALE_RANGE);
     }
 }
@@ -1304,10 +1529,12 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
 __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int32_t cstride, int32_t kstride,
                                      const int32_t* bias, int32_t bias_len, int32_t zx, int32_t zw,
                                      const int32_t* mult, const int32_t* shift, int32_t per_channel, int32_t dbl,
-                                     int32_t out_zp, v4i* tab)
+                                     int32_t out_zp, v4i* tab, int64_t wbatch, int32_t tbatch)
 {
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
+    w += blockIdx.y * wbatch;
+    tab += blockIdx.y * tbatch;
     if (c == 0 && lane == 0) {
         const int32_t zf = int32_t(uint32_t(uint8_t(zx)) * 0x01010101u);
         tab[2 * N] = v4i{zf, zf, zf, zf};
@@ -1357,7 +1584,7 @@ void launch(const ConvI8Args& a, hipStream_t s)
         return true;
     }();
     (void)attr;
-    dim3 grid((a.M + BP - 1) / BP, (a.N + BC - 1) / BC);
+    dim3 grid((a.M + BP - 1) / BP, (a.N + BC - 1) / BC, PW ? a.batch : 1);
     hipLaunchKernelGGL(kfn, grid, dim3(256), lds, s, a);
 }
 
@@ -1386,14 +1613,20 @@ void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
 #undef TOSA_CONV_OB
 }
 
+// Channel tile with the least padded channel work (the 128-channel tile
+// skips a 64-channel half past N), the wider tile on a tie: the epilogue's
+// per-output work dominates layers with few reduction steps.
 template <int KC, bool PW>
 void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
 {
-    if (a.N > 64)
+    const int64_t n = a.N;
+    const int64_t w128 = (n + 63) / 64 * 64, w64 = (n + 63) / 64 * 64, w32 = (n + 31) / 32 * 32,
+                  w16 = (n + 15) / 16 * 16;
+    if (w128 <= w32 && w128 <= w16 && n > 64)
         launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s);
-    else if (a.N > 32)
+    else if (w64 <= w32 && w64 <= w16 && n > 32)
         launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
-    else if (a.N > 16)
+    else if (w32 <= w16 && n > 16)
         launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
     else
         launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
@@ -1627,9 +1860,8 @@ bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& l
 template <int G, int OB, bool RS, bool ZW>
 void launch_dw(const DwArgs& a, hipStream_t s)
 {
-    const unsigned blocks = unsigned((a.P + 63) / 64);
-    hipLaunchKernelGGL((conv_i8_dw_kernel<G, OB, RS, ZW>), dim3(blocks, unsigned((a.C / 16 + 3) / 4)), dim3(256), 0, s,
-                       a);
+    const int64_t items = int64_t((a.P + 63) / 64) * (a.C / 16);
+    hipLaunchKernelGGL((conv_i8_dw_kernel<G, OB, RS, ZW>), dim3(unsigned((items + 3) / 4)), dim3(256), 0, s, a);
 }
 
 template <int G>
@@ -1681,10 +1913,82 @@ void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStre
     // [KH, KW, C, 1] w[k C + c].
     const int32_t K = d.depthwise ? d.kh * d.kw : d.kh * d.kw * d.ic;
     const int32_t cstride = d.depthwise ? 1 : K, kstride = d.depthwise ? d.ic : 1;
-    hipLaunchKernelGGL(conv_i8_table_kernel, dim3(d.oc), dim3(64), 0, stream, d.w, d.oc, K, cstride, kstride, d.bias,
-                       d.bias_len, d.zp_x, d.zp_w, rs ? rs->mult : nullptr, rs ? rs->shift : nullptr,
+    const int batch = d.depthwise ? 1 : d.batch;
+    hipLaunchKernelGGL(conv_i8_table_kernel, dim3(d.oc, batch), dim3(64), 0, stream, d.w, d.oc, K, cstride, kstride,
+                       d.bias, d.bias_len, d.zp_x, d.zp_w, rs ? rs->mult : nullptr, rs ? rs->shift : nullptr,
                        rs ? rs->per_channel : 0, rs ? int32_t(rs->rounding == 3) : 0,
-                       rs ? int32_t(rs->out_zp) : 0, static_cast<v4i*>(tab));
+                       rs ? int32_t(rs->out_zp) : 0, static_cast<v4i*>(tab), int64_t(d.oc) * K,
+                       int32_t(conv_i8_table_stride(d.oc) / 4));
+}
+
+int32_t conv_i8_im2col_kp(const ConvI8Desc& d) { return (d.kh * d.kw * d.ic + 15) / 16 * 16; }
+
+void conv_i8_im2col(const ConvI8Desc& d, int8_t* xcol, hipStream_t stream)
+{
+    Im2colArgs a{};
+    a.x = d.x;
+    a.out = xcol;
+    a.M = d.n * d.oh * d.ow;
+    a.K = d.kh * d.kw * d.ic;
+    a.Kp = conv_i8_im2col_kp(d);
+    a.IC = d.ic;
+    a.ih = d.ih;
+    a.iw = d.iw;
+    a.kw = d.kw;
+    a.ohow = d.oh * d.ow;
+    a.ow = d.ow;
+    a.pt = d.pt;
+    a.pl = d.pl;
+    a.sy = d.sy;
+    a.sx = d.sx;
+    a.dy = d.dy;
+    a.dx = d.dx;
+    a.div_ohow = FastDiv(uint32_t(a.ohow));
+    a.div_ow = FastDiv(uint32_t(d.ow));
+    a.zp_x = d.zp_x;
+    if (a.M <= 0)
+        return;
+    const dim3 grid(unsigned((a.M + 255) / 256), unsigned(a.Kp / 16));
+    if (a.Kp <= IM2COL_TAB) {
+        Im2colTab t{};
+        for (int k = 0; k < a.Kp; k++) {
+            if (k >= a.K) {
+                t.off[k] = -1;
+                continue;
+            }
+            const int tap = k / d.ic, ic = k % d.ic;
+            const int ky = tap / d.kw, kx = tap % d.kw;
+            t.dy[k] = int16_t(ky * d.dy);
+            t.dx[k] = int16_t(kx * d.dx);
+            t.off[k] = (ky * d.dy * d.iw + kx * d.dx) * d.ic + ic;
+        }
+        if (d.ic % 4 == 0 && reinterpret_cast<uintptr_t>(d.x) % 4 == 0)
+            hipLaunchKernelGGL(conv_i8_im2col_tab_kernel<true>, grid, dim3(256), 0, stream, a, t);
+        else
+            hipLaunchKernelGGL(conv_i8_im2col_tab_kernel<false>, grid, dim3(256), 0, stream, a, t);
+        return;
+    }
+    hipLaunchKernelGGL(conv_i8_im2col_kernel, grid, dim3(256), 0, stream, a);
+}
+
+void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t* out, hipStream_t stream)
+{
+    const int64_t n = int64_t(rows) * kp;
+    if (n <= 0)
+        return;
+    hipLaunchKernelGGL(conv_i8_rowpad_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, w, rows, k, kp,
+                       out);
+}
+
+void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream)
+{
+    if (int64_t(batch) * c * w <= 0)
+        return;
+    const dim3 grid(unsigned((w + 63) / 64), unsigned((c + 63) / 64), unsigned(batch));
+    if (w % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0)
+        hipLaunchKernelGGL(transpose_b_kernel<true>, grid, dim3(256), 0, stream, b, c, w, out);
+    else
+        hipLaunchKernelGGL(transpose_b_kernel<false>, grid, dim3(256), 0, stream, b, c, w, out);
 }
 
 int64_t conv_i8_wpack_bytes(const ConvI8Desc& d)
@@ -1738,11 +2042,14 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
         // [lo, hi] (prepare_clamp_int decodes them in that type).
         e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
         e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
+        e.range = rs->min_shift <= 31;
         ob = rs->out_bytes;
     }
     if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)
         return;
     const bool zw = d.zp_w != 0;
+    if (d.depthwise && depthwise_i8_lds(d, tab, rs, out, err, stream))
+        return;
     if (d.depthwise) {
         DwArgs w{};
         w.x = d.x;
@@ -1840,6 +2147,11 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     a.div_ow = FastDiv(uint32_t(d.ow));
     a.zp_x = d.zp_x;
     a.E = e;
+    a.batch = pw ? d.batch : 1;
+    a.bsx = int64_t(a.M) * a.K;
+    a.bsw = int64_t(a.N) * a.K;
+    a.bso = int64_t(a.M) * a.N * ob;
+    a.bst = int32_t(conv_i8_table_stride(d.oc) / 4);
     if (pw) {
         if (a.K >= 128)
             launch_tile<128, true>(a, ob, rs != nullptr, zw, stream);

@@ -370,6 +370,86 @@ __global__ void residual_c4_kernel(RescaleDev ra, RescaleDev rb, RescaleDev ro, 
     report(err, e);
 }
 
+// Residual block with every REQUIRE settled on the host (see
+// residual_fast_ok): a thread owns 4 consecutive channels of the output and
+// walks pixels, with the three RESCALEs' multipliers, shifts and rounding
+// constants for those channels in registers. Per element:
+//   va = apply_scale_32(a - za), vb = apply_scale_32(b - zb)     (int8 -> int32)
+//   y  = clamp(apply_scale_32(va + vb (mod 2^32)) + zo)          (int32 -> int8)
+// with apply_scale_32 (src/ops/quant.rs:17-32) as one 64-bit multiply-add of
+// the sign-selected rounding constant (the output zero point folded into the
+// final one) and an arithmetic shift.
+struct ResChan {
+    int32_t m, s;
+    int64_t rp, rn;
+};
+
+__device__ __forceinline__ ResChan res_chan(const RescaleDev& r, int c, int64_t zp)
+{
+    const int ch = r.per_channel ? c : 0;
+    ResChan q;
+    q.m = r.mult[ch];
+    q.s = r.shift[ch];
+    const int64_t half = int64_t(1) << (q.s - 1);
+    const int64_t d = (r.rounding == 3 && q.s > 31) ? (int64_t(1) << 30) : 0;
+    const int64_t z = zp * (int64_t(1) << q.s);
+    q.rp = half + d + z;
+    q.rn = half - d + z;
+    return q;
+}
+
+__device__ __forceinline__ int32_t res_scale(int32_t x, const ResChan& q)
+{
+    return int32_t((int64_t(x) * q.m + (x >= 0 ? q.rp : q.rn)) >> q.s);
+}
+
+__global__ void __launch_bounds__(256) residual_fast_kernel(RescaleDev ra, RescaleDev rb, RescaleDev ro,
+                                                            const int8_t* a, const int8_t* b, int64_t pixels,
+                                                            int32_t channels, int32_t ppb, int8_t* out,
+                                                            uint32_t* err)
+{
+    const int tpp = channels >> 2;  // threads per pixel
+    const int t = threadIdx.x;
+    if (t >= tpp * ppb)
+        return;
+    const int cq = t % tpp;
+    const int c0 = 4 * cq;
+    ResChan qa[4], qb[4], qo[4];
+    int32_t lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        qa[i] = res_chan(ra, c0 + i, 0);
+        qb[i] = res_chan(rb, c0 + i, 0);
+        qo[i] = res_chan(ro, c0 + i, ro.out_zp);
+        lo[i] = qo[i].s - 1 < 31 ? -(int32_t(1) << (qo[i].s - 1)) : INT32_MIN;
+    }
+    const int32_t za = int32_t(ra.in_zp), zb = int32_t(rb.in_zp);
+    const int32_t clo = int32_t(ro.has_clamp ? (ro.clamp_lo > ro.lo ? ro.clamp_lo : ro.lo) : ro.lo);
+    const int32_t chi = int32_t(ro.has_clamp ? (ro.clamp_hi < ro.hi ? ro.clamp_hi : ro.hi) : ro.hi);
+    bool bad = false;
+    const uint32_t* a4 = reinterpret_cast<const uint32_t*>(a);
+    const uint32_t* b4 = reinterpret_cast<const uint32_t*>(b);
+    uint32_t* o4 = reinterpret_cast<uint32_t*>(out);
+    for (int64_t p = int64_t(blockIdx.x) * ppb + t / tpp; p < pixels; p += int64_t(gridDim.x) * ppb) {
+        const int64_t q = p * tpp + cq;
+        const uint32_t wa = a4[q], wb = b4[q];
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int32_t va = res_scale(int32_t(int8_t(wa >> (8 * i))) - za, qa[i]);
+            const int32_t vb = res_scale(int32_t(int8_t(wb >> (8 * i))) - zb, qb[i]);
+            const int32_t sum = int32_t(uint32_t(va) + uint32_t(vb));
+            bad |= sum < lo[i] || sum > ~lo[i];
+            int32_t r = res_scale(sum, qo[i]);
+            r = r < clo ? clo : (r > chi ? chi : r);
+            packed |= (uint32_t(r) & 0xFFu) << (8 * i);
+        }
+        o4[q] = packed;
+    }
+    if (bad)
+        atomicOr(err, DERR_SCALE_RANGE);
+}
+
 // ---------------------------------------------------------------------------
 // TRANSPOSE: output element i reads input at sum(index_d * stride_perm[d]).
 // ---------------------------------------------------------------------------
@@ -400,6 +480,30 @@ unsigned grid_for(int64_t n)
 }
 
 }  // namespace
+
+// The residual kernel without per-element checks applies when every REQUIRE
+// of the three RESCALEs is settled by the parameters: int8 -> int32 with
+// SINGLE/DOUBLE rounding and shifts >= 9 (|a - za| <= 255 < 2^(s-1), and the
+// scaled value fits int32), int32 -> int8 with SINGLE/DOUBLE rounding and an
+// output zero point that folds into the rounding constant; 4-byte aligned
+// rows of channels % 4 == 0 values, at most 1024 channels.
+static bool residual_fast_ok(const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro, int64_t count,
+                      int64_t channels, const void* a, const void* b, const void* out)
+{
+    auto in_ok = [channels](const RescaleDev& r) {
+        return r.scale32 && (r.rounding == 1 || r.rounding == 3) && r.in_bits == 8 && !r.in_unsigned &&
+               r.out_bytes == 4 && r.out_zp == 0 && !r.has_clamp && r.min_shift >= 9 &&
+               (!r.per_channel || r.channels == channels);
+    };
+    const int64_t zp = ro.out_zp < 0 ? -ro.out_zp : ro.out_zp;
+    const bool fold = zp == 0 || (ro.max_shift <= 60 && zp <= (int64_t(1) << (60 - ro.max_shift)));
+    const bool o_ok = ro.scale32 && (ro.rounding == 1 || ro.rounding == 3) && ro.in_bits == 32 && !ro.in_unsigned &&
+                      ro.in_zp == 0 && ro.out_bytes == 1 && fold && (!ro.per_channel || ro.channels == channels);
+    const bool aligned = (reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                          reinterpret_cast<uintptr_t>(out)) % 4 == 0;
+    return in_ok(ra) && in_ok(rb) && o_ok && aligned && channels % 4 == 0 && channels >= 4 && channels <= 1024 &&
+           count % channels == 0;
+}
 
 bool depthwise_i8_supported(int kh, int kw, int c)
 {
@@ -477,6 +581,15 @@ void residual_add_i8(const RescaleDev& ra, const RescaleDev& rb, const RescaleDe
 {
     if (count <= 0)
         return;
+    if (residual_fast_ok(ra, rb, ro, count, channels, a, b, out)) {
+        const int tpp = int(channels / 4);
+        const int ppb = 256 / tpp;
+        const int64_t pixels = count / channels;
+        const int64_t blocks = (pixels + ppb - 1) / ppb;
+        hipLaunchKernelGGL(residual_fast_kernel, dim3(unsigned(blocks < 8192 ? blocks : 8192)), dim3(256), 0,
+                           stream, ra, rb, ro, a, b, pixels, int32_t(channels), ppb, static_cast<int8_t*>(out), err);
+        return;
+    }
     if (count % 4 == 0 && channels % 4 == 0)
         hipLaunchKernelGGL(residual_c4_kernel, dim3(grid_for(count / 4)), dim3(256), 0, stream, ra, rb, ro, a, b,
                            count / 4, channels, static_cast<int8_t*>(out), err);

@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "../device.h"
@@ -12,6 +13,24 @@
 
 namespace tosa {
 namespace kern {
+
+// Median of three (v_med3_i32): clamp of v to [lo, hi] when lo <= hi.
+__device__ __forceinline__ int32_t med3_i32(int32_t v, int32_t lo, int32_t hi)
+{
+    int32_t r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(lo), "v"(hi));
+    return r;
+}
+
+// Four values' low bytes packed into one word: two byte permutes (v_perm_b32
+// selector bytes 0-3 pick the second operand, 4-7 the first, 0x0c gives 0)
+// and an OR.
+__device__ __forceinline__ uint32_t pack4_u8(int32_t v0, int32_t v1, int32_t v2, int32_t v3)
+{
+    const uint32_t lo = __builtin_amdgcn_perm(uint32_t(v1), uint32_t(v0), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(uint32_t(v3), uint32_t(v2), 0x04000c0cu);
+    return lo | hi;
+}
 
 // q = n / d for n < 2^31: (mulhi(n, m) + n) >> s.
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }

@@ -226,8 +226,8 @@ StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* b
     std::string key;
     if (cacheable) {
         char buf[192];
-        std::snprintf(buf, sizeof buf, "conv_i8_tab:%p:%d:%d:%d:%p:%p:%d:%d:%lld", bias_key, d.bias_len, d.zp_x,
-                      d.zp_w, rs ? static_cast<const void*>(rs->mult) : nullptr,
+        std::snprintf(buf, sizeof buf, "conv_i8_tab:%d:%p:%d:%d:%d:%p:%p:%d:%d:%lld", d.batch, bias_key, d.bias_len,
+                      d.zp_x, d.zp_w, rs ? static_cast<const void*>(rs->mult) : nullptr,
                       rs ? static_cast<const void*>(rs->shift) : nullptr, rs ? rs->per_channel : 0,
                       rs ? rs->rounding : 0, rs ? static_cast<long long>(rs->out_zp) : 0LL);
         key = buf;
@@ -236,7 +236,7 @@ StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* b
         if (it != wstore.derived.end())
             return it->second;
     }
-    auto t = make_device_storage(DT_INT32, conv_i8_table_words(d.oc));
+    auto t = make_device_storage(DT_INT32, conv_i8_table_words(d.oc, d.batch));
     conv_i8_table(d, rs, t->device_out(), s);
     if (cacheable) {
         hip_check(hipStreamSynchronize(s), "conv_i8 table");
@@ -265,6 +265,28 @@ StoragePtr conv_i8_wpack_for(const ConvI8Desc& d, Storage& wstore, bool cacheabl
     conv_i8_wpack(d, t->device_out(), s);
     if (cacheable) {
         hip_check(hipStreamSynchronize(s), "conv_i8 weight pack");
+        std::lock_guard<std::mutex> lk(derived_mu());
+        wstore.derived[key] = t;
+    }
+    return t;
+}
+
+// Device data derived from a weight-like operand by `make` (an int8 buffer
+// of `bytes`), cached on its storage under `key` when the operand is a graph
+// constant.
+StoragePtr derived_i8(Storage& wstore, const std::string& key, int64_t bytes, bool cacheable, hipStream_t s,
+                      const std::function<void(void*)>& make)
+{
+    if (cacheable) {
+        std::lock_guard<std::mutex> lk(derived_mu());
+        auto it = wstore.derived.find(key);
+        if (it != wstore.derived.end())
+            return it->second;
+    }
+    auto t = make_device_storage(DT_INT8, bytes);
+    make(t->device_out());
+    if (cacheable) {
+        hip_check(hipStreamSynchronize(s), key.c_str());
         std::lock_guard<std::mutex> lk(derived_mu());
         wstore.derived[key] = t;
     }
@@ -372,8 +394,11 @@ RescalePrep prepare_rescale(const ExecState& st, const Operator& op, const Tenso
     r.in_zp = izp;
     r.out_zp = ozp;
     r.max_shift = 2;
-    for (int64_t c = 0; c < channels; c++)
+    r.min_shift = 62;
+    for (int64_t c = 0; c < channels; c++) {
         r.max_shift = std::max<int32_t>(r.max_shift, int32_t(sv[c]));
+        r.min_shift = std::min<int32_t>(r.min_shift, int32_t(sv[c]));
+    }
     if (a.output_unsigned) {
         r.lo = 0;
         r.hi = (int64_t(1) << bit_width(out_t)) - 1;
@@ -870,6 +895,31 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
                 conv_i8_fast(f, tab->device_in(), rs, out, err, s);
                 return;
             }
+            if (mfma_int && !fast && (!rs || conv_i8_fast_epilogue_ok(*rs)) &&
+                int64_t(fd.n) * fd.oh * fd.ow * conv_i8_im2col_kp(fd) < (int64_t(1) << 31)) {
+                // Channels or geometry the tiled kernels do not take: a
+                // pointwise GEMM over the materialised im2col.
+                auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), rs, wb_const && (!rs || rs_const), s);
+                const int32_t K = fd.kh * fd.kw * fd.ic, kp = conv_i8_im2col_kp(fd);
+                auto wp = derived_i8(*weight->data, "conv_i8_rowpad:" + std::to_string(kp), int64_t(fd.oc) * kp,
+                                     w_const, s, [&](void* dst) {
+                                         conv_i8_rowpad(fd.w, fd.oc, K, kp, static_cast<int8_t*>(dst), s);
+                                     });
+                auto xcol = make_device_storage(DT_INT8, int64_t(fd.n) * fd.oh * fd.ow * kp);
+                conv_i8_im2col(fd, static_cast<int8_t*>(xcol->device_out()), s);
+                ConvI8Desc p = fd;
+                p.x = static_cast<const int8_t*>(xcol->device_in());
+                p.w = static_cast<const int8_t*>(wp->device_in());
+                p.ih = fd.oh;
+                p.iw = fd.ow;
+                p.ic = kp;
+                p.kh = p.kw = 1;
+                p.pt = p.pl = 0;
+                p.sy = p.sx = p.dy = p.dx = 1;
+                p.wpack = nullptr;
+                conv_i8_fast(p, tab->device_in(), rs, out, err, s);
+                return;
+            }
             if (fast && !mfma_int && !depthwise_i8_supported(fd.kh, fd.kw, fd.ic)) {
                 // A RESCALE the fused epilogue does not take, on a depthwise
                 // shape only the MFMA kernel handles: int32 result, then the
@@ -1068,6 +1118,60 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
     const bool mfma_int = out_t == DT_INT32 && small;
     const bool mfma_float = !is_int && out_t == DT_FP32 && !st.opts.strict_float && small &&
                             ((a_t == DT_BF16 && b_t == DT_BF16) || (a_t == DT_FP16 && b_t == DT_FP16));
+    const void* a_dev = (mfma_int && c % 16 == 0) ? a->data->device_in() : nullptr;
+    if (a_dev && reinterpret_cast<uintptr_t>(a_dev) % 16 == 0) {
+        // int8: the pointwise tiled kernel, one batch per grid slice, over B
+        // transposed to rows of c bytes (cached when B is a graph constant);
+        // zero points folded into the accumulator like CONV2D's.
+        const bool b_const = st.const_defs.count(op.inputs[1]) != 0;
+        ConvI8Desc fd;
+        fd.x = static_cast<const int8_t*>(a_dev);
+        fd.bias = nullptr;
+        fd.bias_len = 1;
+        fd.n = 1;
+        fd.ih = fd.oh = int32_t(h);
+        fd.iw = fd.ow = 1;
+        fd.ic = int32_t(c);
+        fd.oc = int32_t(w);
+        fd.zp_x = int32_t(azp);
+        fd.zp_w = int32_t(bzp);
+        fd.batch = int32_t(n);
+        auto launch = [fd, a, b, b_const](void* out, const RescaleDev* rs, bool rs_const, uint32_t* err,
+                                          hipStream_t s) {
+            ConvI8Desc d = fd;
+            auto bt = derived_i8(*b->data, "matmul_bt", int64_t(d.batch) * d.ic * d.oc, b_const, s, [&](void* dst) {
+                transpose_b_i8(static_cast<const int8_t*>(b->data->device_in()), d.batch, d.ic, d.oc,
+                               static_cast<int8_t*>(dst), s);
+            });
+            d.w = static_cast<const int8_t*>(bt->device_in());
+            auto tab = conv_i8_table_for(d, *b->data, nullptr, rs, b_const && (!rs || rs_const), s);
+            conv_i8_fast(d, tab->device_in(), rs, out, err, s);
+        };
+        if (auto tail = plan_tail(st, index, out_shape)) {
+            if (conv_i8_fast_epilogue_ok(tail->rp.rs)) {
+                auto fin =
+                    new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], out_shape, tail->rp.out_t);
+                const bool rs_const =
+                    st.const_defs.count(tail->rop->inputs[1]) && st.const_defs.count(tail->rop->inputs[2]);
+                if (count > 0)
+                    launch(fin->data->device_out(), &tail->rp.rs, rs_const, st.err(), st.s());
+                auto keep = tail->rp.params;
+                finish_fused(st, out_name, out_shape, *tail, fin, [launch, keep](Storage& o) {
+                    Stream& s = thread_stream();
+                    if (o.count > 0)
+                        launch(o.device_out(), nullptr, false, s.err, s.s);
+                    else
+                        o.device_out();
+                });
+                return;
+            }
+        }
+        auto out = new_output(out_name, out_shape, DT_INT32);
+        if (count > 0)
+            launch(out->data->device_out(), nullptr, false, st.err(), st.s());
+        st.set(out);
+        return;
+    }
     if (mfma_int || mfma_float) {
         GemmDesc gd;
         gd.is_conv = 0;
