@@ -439,3 +439,75 @@ def test_avg_pool_int8_paths(c):
         graph = g.build(["y"])
         ins = {"x": (x, "INT8")}
         assert same_int(run(graph, ins)["y"].numpy(), oracle_run(graph, ins)["y"].vals), (k, s, pad)
+
+
+# ---------------------------------------------------------------------------
+# bf16 / fp16 GEMM kernel (K a multiple of 64): batched MATMUL with B as
+# [K][N] and 1x1 CONV2D with the float epilogue. fp32 accumulation in another
+# order than the reference's: |y - exact| <= 2 K 2^-24 sum|a b| (+ the output
+# rounding and the bias add for narrow outputs).
+# ---------------------------------------------------------------------------
+def _f16_to_torch(bits, dtype):
+    import torch
+    t = torch.from_numpy(bits.view(np.int16))
+    return t.view(torch.bfloat16 if dtype == "BF16" else torch.float16).double()
+
+
+@pytest.mark.parametrize("dtype", ["BF16", "FP16"])
+@pytest.mark.parametrize("dims", [(2, 300, 128, 264), (1, 64, 1280, 1000), (3, 257, 64, 8), (1, 512, 192, 520)])
+def test_gemm_f16_matmul(dtype, dims):
+    import torch
+    batch, h, c, w = dims
+    r = np.random.default_rng(sum(dims) + len(dtype))
+    a = W._normal(r, (batch, h, c), dtype)
+    b = W._normal(r, (batch, c, w), dtype)
+    g = GraphBuilder()
+    g.input("a", a.shape, dtype)
+    g.input("b", b.shape, dtype)
+    g.const("az", np.array([0], np.uint16), dtype)
+    g.const("bz", np.array([0], np.uint16), dtype)
+    g.tensor("y", [batch, h, w], "FP32")
+    g.op("MATMUL", ["a", "b", "az", "bz"], ["y"])
+    y = run(g.build(["y"]), {"a": (a, dtype), "b": (b, dtype)})["y"].numpy().astype(np.float64)
+    ta, tb = _f16_to_torch(a, dtype), _f16_to_torch(b, dtype)
+    exact = torch.bmm(ta, tb).numpy()
+    absy = torch.bmm(ta.abs(), tb.abs()).numpy()
+    assert np.all(np.abs(y - exact) <= 2 * c * 2.0 ** -24 * absy), np.abs(y - exact).max()
+
+
+@pytest.mark.parametrize("dtype,out_dtype", [("BF16", "FP32"), ("FP16", "FP32"), ("BF16", "BF16"), ("FP16", "FP16")])
+@pytest.mark.parametrize("shape", [(2, 13, 17, 128, 200), (1, 28, 28, 64, 512), (3, 5, 7, 256, 24)])
+def test_gemm_f16_conv1x1(dtype, out_dtype, shape):
+    import torch
+    n, h, w_, cin, cout = shape
+    r = np.random.default_rng(sum(shape) + len(dtype) + len(out_dtype))
+    x = W._normal(r, (n, h, w_, cin), dtype)
+    wt = W._normal(r, (cout, 1, 1, cin), dtype)
+    g = GraphBuilder()
+    g.input("x", x.shape, dtype)
+    g.const("w", wt, dtype)
+    if out_dtype == "FP32":
+        bias = r.standard_normal(cout).astype(np.float32)
+        g.const("bias", bias, "FP32")
+        bias_f = bias.astype(np.float64)
+    else:
+        bias_bits = W._normal(r, (cout,), out_dtype)
+        g.const("bias", bias_bits, out_dtype)
+        bias_f = _f16_to_torch(bias_bits, out_dtype).numpy()
+    g.const("zx", np.array([0], np.uint16), dtype)
+    g.const("zw", np.array([0], np.uint16), dtype)
+    g.tensor("y", [n, h, w_, cout], out_dtype)
+    g.op("CONV2D", ["x", "w", "bias", "zx", "zw"], ["y"], pad=[0, 0, 0, 0], stride=[1, 1], dilation=[1, 1],
+         acc_type="FP32")
+    got = run(g.build(["y"]), {"x": (x, dtype)})["y"].numpy()
+    if out_dtype != "FP32":
+        got = _f16_to_torch(got.view(np.uint16), out_dtype).numpy()
+    got = got.astype(np.float64).reshape(-1, cout)
+    tx = _f16_to_torch(x, dtype).reshape(-1, cin)
+    tw = _f16_to_torch(wt, dtype).reshape(cout, cin)
+    acc = (tx @ tw.T).numpy()
+    absy = (tx.abs() @ tw.abs().T).numpy()
+    exact = acc + bias_f
+    u = {"FP32": 0.0, "BF16": 2.0 ** -8, "FP16": 2.0 ** -11}[out_dtype]
+    bound = 2 * cin * 2.0 ** -24 * absy + 2.0 ** -24 * np.abs(exact) + 2 * u * (np.abs(acc) + np.abs(exact)) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound), np.abs(got - exact).max()

@@ -150,6 +150,26 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
                   hipStream_t stream);
 
 // ---------------------------------------------------------------------------
+// bf16 / fp16 GEMM with fp32 accumulation (gemm_f16.hip)
+// ---------------------------------------------------------------------------
+// C[b][m][n] = sum_k A[b][m][k] B[b][k][n] (b_kn: B as [K][N], the MATMUL
+// right operand) or sum_k A[b][m][k] B[b][n][k] (OHWI 1x1 weights), then
+// out = round(round(C) + bias[n]) in out_fmt when a bias is given (the
+// CONV2D float epilogue), else C rounded to out_fmt.
+struct GemmF16Desc {
+    int32_t batch = 1, m = 1, n = 1, k = 1;
+    GemmElem elem = ELEM_BF16;
+    bool b_kn = true;
+    const void* bias = nullptr;  // f32 [bias_len], bias_len 1 or n
+    int32_t bias_len = 1;
+    FloatFmt out_fmt = FMT_F32;
+};
+// K a multiple of 64, 16-byte aligned operands, N % 8 == 0 for a [K][N] B,
+// every matrix below 2^31 elements.
+bool gemm_f16_supported(int64_t batch, int64_t m, int64_t n, int64_t k, bool b_kn, const void* a, const void* b);
+void gemm_f16(const GemmF16Desc& d, const void* a, const void* b, void* out, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
 // Reference-order kernels (one thread per output, the reference's loop
 // order and rounding, so float results are bit-identical to a sequential
 // evaluation). They cover every type combination the MFMA path does not.

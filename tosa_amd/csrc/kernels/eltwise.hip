@@ -196,21 +196,28 @@ __global__ void avg_pool_i8_c4_kernel(PoolDesc d, const int8_t* x, int8_t* out, 
     r /= d.ow;
     const int oy = int(r % d.oh);
     const int b = int(r / d.oh);
+    // The in-bounds part of the window (padding positions are excluded from
+    // the sum and the count), walked as one flat loop so that many of its
+    // loads are in flight at once.
+    const int y0 = oy * d.sy - d.pt, x0 = ox * d.sx - d.pl;
+    const int ky0 = y0 < 0 ? -y0 : 0, ky1 = d.kh < d.ih - y0 ? d.kh : d.ih - y0;
+    const int kx0 = x0 < 0 ? -x0 : 0, kx1 = d.kw < d.iw - x0 ? d.kw : d.iw - x0;
+    const int wv = kx1 - kx0;
+    const int32_t count = ky1 > ky0 && wv > 0 ? (ky1 - ky0) * wv : 0;
     uint32_t acc[4] = {0, 0, 0, 0};
-    int32_t count = 0;
-    for (int ky = 0; ky < d.kh; ky++) {
-        const int y = oy * d.sy - d.pt + ky;
-        if (y < 0 || y >= d.ih)
-            continue;
-        for (int kx = 0; kx < d.kw; kx++) {
-            const int xx = ox * d.sx - d.pl + kx;
-            if (xx < 0 || xx >= d.iw)
-                continue;
-            const uint32_t wv = *reinterpret_cast<const uint32_t*>(x + ((int64_t(b) * d.ih + y) * d.iw + xx) * d.c + c0);
+    if (count > 0) {
+        const int8_t* base = x + ((int64_t(b) * d.ih + y0 + ky0) * d.iw + x0 + kx0) * d.c + c0;
+        int row = 0, col = 0;
+#pragma unroll 16
+        for (int t = 0; t < count; t++) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(base + (int64_t(row) * d.iw + col) * d.c);
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                acc[j] += uint32_t(int32_t(int8_t(wv >> (8 * j))) - int32_t(d.in_zp));
-            count++;
+                acc[j] += uint32_t(int32_t(int8_t(v >> (8 * j))) - int32_t(d.in_zp));
+            if (++col == wv) {
+                col = 0;
+                row++;
+            }
         }
     }
     const uint32_t c1 = uint32_t(count) - 1u;

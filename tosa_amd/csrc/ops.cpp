@@ -1003,8 +1003,25 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         gd.out_fmt = FloatFmt(fmt_code(out_t));
         auto out = new_output(out_name, g.out_shape, out_t);
         void* od = out->data->device_out();
-        if (count > 0)
-            kern::gemm(gd, input->data->device_in(), weight->data->device_in(), od, st.err(), st.s());
+        const void* xd = input->data->device_in();
+        const void* wd = weight->data->device_in();
+        const bool pw = g.kh == 1 && g.kw == 1 && g.sy == 1 && g.sx == 1 && g.pt == 0 && g.pl == 0 && g.ih == g.oh &&
+                        g.iw == g.ow;
+        if (count > 0 && pw && kern::gemm_f16_supported(1, g.n * g.oh * g.ow, g.oc, g.ic, false, xd, wd)) {
+            // 1x1 convolution: NHWC rows x OHWI rows on the dedicated GEMM.
+            GemmF16Desc fd;
+            fd.m = int32_t(g.n * g.oh * g.ow);
+            fd.n = int32_t(g.oc);
+            fd.k = int32_t(g.ic);
+            fd.elem = gd.elem;
+            fd.b_kn = false;
+            fd.bias = gd.bias;
+            fd.bias_len = gd.bias_len;
+            fd.out_fmt = gd.out_fmt;
+            kern::gemm_f16(fd, xd, wd, od, st.s());
+        } else if (count > 0) {
+            kern::gemm(gd, xd, wd, od, st.err(), st.s());
+        }
         st.set(out);
         return;
     }
@@ -1169,6 +1186,21 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
         auto out = new_output(out_name, out_shape, DT_INT32);
         if (count > 0)
             launch(out->data->device_out(), nullptr, false, st.err(), st.s());
+        st.set(out);
+        return;
+    }
+    if (mfma_float && count > 0 &&
+        kern::gemm_f16_supported(n, h, w, c, true, a->data->device_in(), b->data->device_in())) {
+        GemmF16Desc fd;
+        fd.batch = int32_t(n);
+        fd.m = int32_t(h);
+        fd.n = int32_t(w);
+        fd.k = int32_t(c);
+        fd.elem = a_t == DT_BF16 ? ELEM_BF16 : ELEM_F16;
+        fd.b_kn = true;
+        fd.out_fmt = FMT_F32;
+        auto out = new_output(out_name, out_shape, out_t);
+        kern::gemm_f16(fd, a->data->device_in(), b->data->device_in(), out->data->device_out(), st.s());
         st.set(out);
         return;
     }
