@@ -1303,52 +1303,65 @@ __global__ void conv_i8_rowpad_kernel(const int8_t* w, int32_t rows, int32_t K, 
 }
 
 // B [batch][C][W] -> [batch][W][C] (the MATMUL right operand as OHWI-style
-// rows of C bytes), 64 x 64 byte tiles through LDS. C % 16 == 0; VEC: W % 16
-// == 0, so the rows of B load as 16-byte vectors.
+// rows of C bytes): a workgroup moves TT 64 x 64 byte tiles along W through
+// LDS, all of their loads issued before the first LDS write. C % 16 == 0;
+// VEC: W % 16 == 0, so the rows of B load as 16-byte vectors.
+constexpr int TR_TT = 4;
+
 template <bool VEC>
 __global__ void __launch_bounds__(256) transpose_b_kernel(const int8_t* b, int32_t C, int32_t W, int8_t* out)
 {
-    __shared__ uint8_t t[64][64 + 4];
+    __shared__ uint8_t t[TR_TT][64][64 + 4];
     const int z = blockIdx.z;
-    const int c0 = blockIdx.y * 64, w0 = blockIdx.x * 64;
+    const int c0 = blockIdx.y * 64, w00 = blockIdx.x * (64 * TR_TT);
     const int8_t* src = b + int64_t(z) * C * W;
     int8_t* dst = out + int64_t(z) * C * W;
     const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
-    // load: row c0 + r, columns w0 + 16 q .. + 15
-    {
-        const int c = c0 + r;
-        const int w = w0 + 16 * q;
-        uint32_t v[4] = {0, 0, 0, 0};
+    // load: row c0 + r, columns w0 + 16 q .. + 15 of each tile
+    uint32_t v[TR_TT][4];
+    const int c = c0 + r;
+#pragma unroll
+    for (int tt = 0; tt < TR_TT; tt++) {
+        const int w = w00 + 64 * tt + 16 * q;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            v[tt][j] = 0;
         if (c < C) {
             if (VEC) {
                 if (w < W) {
                     const v4u x = *reinterpret_cast<const v4u*>(src + int64_t(c) * W + w);
-                    v[0] = x.x;
-                    v[1] = x.y;
-                    v[2] = x.z;
-                    v[3] = x.w;
+                    v[tt][0] = x.x;
+                    v[tt][1] = x.y;
+                    v[tt][2] = x.z;
+                    v[tt][3] = x.w;
                 }
             } else {
 #pragma unroll
                 for (int j = 0; j < 16; j++)
                     if (w + j < W)
-                        v[j >> 2] |= uint32_t(uint8_t(src[int64_t(c) * W + w + j])) << (8 * (j & 3));
+                        v[tt][j >> 2] |= uint32_t(uint8_t(src[int64_t(c) * W + w + j])) << (8 * (j & 3));
             }
         }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TR_TT; tt++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            *reinterpret_cast<uint32_t*>(&t[r][16 * q + 4 * j]) = v[j];
-    }
+            *reinterpret_cast<uint32_t*>(&t[tt][r][16 * q + 4 * j]) = v[tt][j];
     __syncthreads();
-    // store: output row w0 + r, columns c0 + 16 q .. + 15
-    const int w = w0 + r, c = c0 + 16 * q;
-    if (w >= W || c >= C)
-        return;
-    uint32_t v[4] = {0, 0, 0, 0};
+    // store: output row w0 + r, columns c0 + 16 q .. + 15 of each tile
+    const int cc = c0 + 16 * q;
 #pragma unroll
-    for (int j = 0; j < 16; j++)
-        v[j >> 2] |= uint32_t(t[16 * q + j][r]) << (8 * (j & 3));
-    *reinterpret_cast<v4u*>(dst + int64_t(w) * C + c) = v4u{v[0], v[1], v[2], v[3]};
+    for (int tt = 0; tt < TR_TT; tt++) {
+        const int w = w00 + 64 * tt + r;
+        if (w >= W || cc >= C)
+            continue;
+        uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            o[j >> 2] |= uint32_t(t[tt][16 * q + j][r]) << (8 * (j & 3));
+        *reinterpret_cast<v4u*>(dst + int64_t(w) * C + cc) = v4u{o[0], o[1], o[2], o[3]};
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1540,9 +1553,22 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
         tab[2 * N] = v4i{zf, zf, zf, zf};
     }
     int32_t s = 0;
-    if (zx != 0)
-        for (int k = lane; k < K; k += 64)
-            s += w[int64_t(c) * cstride + int64_t(k) * kstride];
+    if (zx != 0) {
+        const int8_t* wr = w + int64_t(c) * cstride;
+        if (kstride == 1 && K % 16 == 0 && reinterpret_cast<uintptr_t>(wr) % 16 == 0) {
+            // Contiguous rows: 16 bytes per lane per step, summed with dot4.
+            for (int k = 16 * lane; k < K; k += 16 * 64) {
+                const v4u v = *reinterpret_cast<const v4u*>(wr + k);
+                s = __builtin_amdgcn_sdot4(int(v.x), 0x01010101, s, false);
+                s = __builtin_amdgcn_sdot4(int(v.y), 0x01010101, s, false);
+                s = __builtin_amdgcn_sdot4(int(v.z), 0x01010101, s, false);
+                s = __builtin_amdgcn_sdot4(int(v.w), 0x01010101, s, false);
+            }
+        } else {
+            for (int k = lane; k < K; k += 64)
+                s += wr[int64_t(k) * kstride];
+        }
+    }
     for (int off = 32; off > 0; off >>= 1)
         s += __shfl_xor(s, off);
     if (lane != 0)
@@ -1984,7 +2010,7 @@ void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t
 {
     if (int64_t(batch) * c * w <= 0)
         return;
-    const dim3 grid(unsigned((w + 63) / 64), unsigned((c + 63) / 64), unsigned(batch));
+    const dim3 grid(unsigned((w + 64 * TR_TT - 1) / (64 * TR_TT)), unsigned((c + 63) / 64), unsigned(batch));
     if (w % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0)
         hipLaunchKernelGGL(transpose_b_kernel<true>, grid, dim3(256), 0, stream, b, c, w, out);
     else
