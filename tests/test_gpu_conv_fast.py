@@ -454,3 +454,84 @@ def test_depthwise_lds_tiles(case):
         for fusion in (True, False):
             got = run(graph, ins, fusion)[out].numpy()
             assert np.array_equal(got.reshape(-1).astype(np.int64), ref.reshape(-1).astype(np.int64)), (out, fusion)
+
+
+# The epilogue table proves apply_scale_32's range REQUIRE unfailable when
+# every channel with a shift below 32 has |bias| + max|x - zx| sum|w - zw|
+# below 2^(shift-1); the kernels then skip the per-value check. Channel 0 is
+# built to meet that bound exactly at one output pixel (every product at
+# max|x - zx| |w - zw|): with the bound at 2^(shift-1) - 1 the table proves
+# the range and the result must equal the oracle's; with the bias one higher
+# the value is 2^(shift-1), the REQUIRE fails and the kernel must report it.
+RANGE_EDGE = [
+    # kind, n, h, w, ic, oc, k, stride, pad, zx, zw
+    ("halo", 1, 28, 28, 64, 64, 3, 1, 1, 5, 3),
+    ("tiled", 1, 17, 17, 64, 32, 3, 2, 1, 0, 0),
+    ("pointwise", 1, 16, 16, 64, 48, 1, 1, 0, -7, 2),
+    ("depthwise_lds", 1, 28, 28, 32, 32, 3, 1, 1, 4, -2),
+    ("depthwise", 2, 9, 9, 16, 16, 3, 1, 1, 0, 0),
+]
+
+
+def _range_edge(case, over, bias_input=False):
+    kind, n, h, w_, ic, oc, k, stride, pad, zx, zw = RANGE_EDGE[case]
+    rng = np.random.default_rng(900 + case)
+    dw = kind.startswith("depthwise")
+    K = k * k * (1 if dw else ic)
+    # The input value that attains max|x - zx|, and the weight step that
+    # makes its product positive.
+    xe, step = (-128, -1) if 128 + zx >= 127 - zx else (127, 1)
+    xmax = abs(xe - zx)
+    s = int(np.floor(np.log2(xmax * K))) if K * xmax < 2 ** 14 else 17
+    T = 2 ** (s - 1)
+    na = (T - 1) // xmax
+    assert 0 < na <= K
+    b0 = T - 1 - na * xmax
+    x = rng.integers(-128, 128, size=(n, h, w_, ic)).astype(np.int8)
+    cy, cx = h // 2, w_ // 2
+    x[0, cy - k // 2:cy + k // 2 + 1, cx - k // 2:cx + k // 2 + 1, :] = xe
+    # Rows of K weights per channel: channel 0 has na active entries, the
+    # others fewer, with random signs.
+    rows = np.full((oc, K), zw, np.int64)
+    rows[0, :na] = zw + step
+    for c in range(1, oc):
+        m = int(rng.integers(0, na))
+        rows[c, rng.choice(K, size=m, replace=False)] = zw + rng.choice([-1, 1], size=m)
+    bias = rng.integers(-50, 50, size=oc).astype(np.int32)
+    bias[0] = b0 + (1 if over else 0)
+    rs = (np.full(oc, 2 ** (s - 7) if s > 7 else 1), np.full(oc, s), 0, False, True)
+    if dw:
+        w = rows.T.reshape(k, k, ic, 1).astype(np.int8)
+        graph = dw_graph(x, w, bias, zx, zw, [pad] * 4, [stride] * 2, (rs[0], rs[1], 0))
+        out = "q"
+    else:
+        w = rows.reshape(oc, k, k, ic).astype(np.int8)
+        graph, out = build(x, w, bias, zx, zw, [pad] * 4, [stride] * 2, [1, 1], rescale=rs, bias_input=bias_input)
+    ins = {"x": (x, "INT8")}
+    if bias_input:
+        ins["b"] = (bias, "INT32")
+    return graph, out, ins
+
+
+@pytest.mark.parametrize("case", range(len(RANGE_EDGE)))
+def test_range_bound_proved(case):
+    graph, out, ins = _range_edge(case, over=False)
+    check(graph, out, ins)
+
+
+@pytest.mark.parametrize("case", range(len(RANGE_EDGE)))
+def test_range_bound_exceeded(case):
+    graph, out, ins = _range_edge(case, over=True)
+    with pytest.raises(O.OracleError):
+        oracle_run(graph, ins)
+    with pytest.raises(T.TosaError) as e:
+        run(graph, ins)
+    assert e.value.kind == "GraphError"
+
+
+@pytest.mark.parametrize("case", [0, 1, 2])
+def test_range_bound_runtime_bias(case):
+    """A bias that is a graph input keeps the table uncached: the per-value
+    check stays on, values inside the range pass."""
+    graph, out, ins = _range_edge(case, over=False, bias_input=True)
+    check(graph, out, ins)

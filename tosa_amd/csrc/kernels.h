@@ -100,6 +100,9 @@ struct ConvI8Desc {
     // the table [batch][conv_i8_table_stride(oc)]. A batched MATMUL runs as
     // this with B transposed to rows of C bytes.
     int32_t batch = 1;
+    // The epilogue table proved that no value can fail apply_scale_32's
+    // range REQUIRE (conv_i8_table_range_safe), so the kernels skip it.
+    bool range_safe = false;
 };
 // Geometry and alignment the kernels handle: CONV2D 1x1 stride-1 unpadded
 // with ic % 16 == 0, any other CONV2D geometry with ic % 64 == 0;
@@ -125,6 +128,11 @@ inline int64_t conv_i8_table_words(int32_t oc, int32_t batch)
     return int64_t(batch - 1) * conv_i8_table_stride(oc) + conv_i8_table_words(oc);
 }
 void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStream_t stream);
+// True when the table (complete on the device) marks every channel whose
+// shift is below 32 as unable to fail apply_scale_32's range REQUIRE: the
+// channel's bound |bias| + max|x - zx| sum_k |w - zw| lies below 2^(shift-1).
+// Copies the table to the host (synchronous).
+bool conv_i8_table_range_safe(const ConvI8Desc& d, const void* tab);
 // Bytes of the packed weight layout of the stride-1 halo kernel for `d`, 0
 // when that kernel does not run for `d`; conv_i8_wpack writes it from d.w.
 int64_t conv_i8_wpack_bytes(const ConvI8Desc& d);

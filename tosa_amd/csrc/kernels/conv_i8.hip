@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include <type_traits>
+#include <vector>
 
 #include "kcommon.h"
 
@@ -827,98 +828,109 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
                 t1[i] = s_tab[2 * (cl + i) + 1];
         }
     };
-    v4i tn0[4], tn1[4];
-    ld_tab(0, tn0, tn1);
+    // RC: apply_scale_32's value-range REQUIRE is checked (some channel's
+    // shift is below 32 and the table could not rule a failure out).
+    auto body = [&](auto rc) {
+        constexpr bool RC = RS && decltype(rc)::value;
+        v4i tn0[4], tn1[4];
+        ld_tab(0, tn0, tn1);
 #pragma unroll
-    for (int a = 0; a < TA; a++) {
-        const int cl = 32 * a + 16 * h;  // tile channel of element 0
-        uint32_t res[TB][4 * OB];
+        for (int a = 0; a < TA; a++) {
+            const int cl = 32 * a + 16 * h;  // tile channel of element 0
+            uint32_t res[TB][4 * OB];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            __builtin_amdgcn_sched_barrier(0);
-            v4i t0[4], t1[4];
-            int32_t hi[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                t0[i] = tn0[i];
-                t1[i] = tn1[i];
-                hi[i] = ~t0[i].z;
-            }
-            if (4 * a + g + 1 < 4 * TA)
-                ld_tab(4 * a + g + 1, tn0, tn1);
-#pragma unroll
-            for (int b = 0; b < TB; b++) {
-                int32_t v[4];
+            for (int g = 0; g < 4; g++) {
+                __builtin_amdgcn_sched_barrier(0);
+                v4i t0[4], t1[4];
+                int32_t hi[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int32_t x = int32_t(uint32_t(acc[a][b][4 * g + i]) - uint32_t(zwx[b]));
-                    if constexpr (RS) {
-                        // Same arithmetic as epilogue(): range REQUIRE of
-                        // apply_scale_32, 64-bit scale with the per-sign
-                        // rounding constant, output zero point and clamp.
-                        bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(x, t0[i].z, hi[i])),
-                                                               uint32_t(x), 0xf6);  // bad | (med3 ^ x)
-                        const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
-                        const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
-                        const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
-                        v[i] = med3(r, E.clo, E.chi);  // output zero point folded into rp, rn
-                    } else {
-                        v[i] = x;
-                    }
+                    t0[i] = tn0[i];
+                    t1[i] = tn1[i];
+                    if constexpr (RC)
+                        hi[i] = ~t0[i].z;
                 }
-                if constexpr (OB == 1) {
-                    // Low bytes of v0..v3 (v_perm_b32: selector bytes 0-3
-                    // pick the second operand, 4-7 the first, 0x0c zero).
-                    const uint32_t p01 = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x0c0c0400u);
-                    const uint32_t p23 = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x0c0c0400u);
-                    res[b][g] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
-                } else if constexpr (OB == 2) {
-                    res[b][2 * g] = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u);
-                    res[b][2 * g + 1] = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u);
+                if (4 * a + g + 1 < 4 * TA)
+                    ld_tab(4 * a + g + 1, tn0, tn1);
+#pragma unroll
+                for (int b = 0; b < TB; b++) {
+                    int32_t v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int32_t x = int32_t(uint32_t(acc[a][b][4 * g + i]) - uint32_t(zwx[b]));
+                        if constexpr (RS) {
+                            // Same arithmetic as epilogue(): range REQUIRE of
+                            // apply_scale_32, 64-bit scale with the per-sign
+                            // rounding constant, output zero point and clamp.
+                            if constexpr (RC)
+                                bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(x, t0[i].z, hi[i])),
+                                                                       uint32_t(x), 0xf6);  // bad | (med3 ^ x)
+                            const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
+                            const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
+                            const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
+                            v[i] = med3(r, E.clo, E.chi);  // output zero point folded into rp, rn
+                        } else {
+                            v[i] = x;
+                        }
+                    }
+                    if constexpr (OB == 1) {
+                        // Low bytes of v0..v3 (v_perm_b32: selector bytes 0-3
+                        // pick the second operand, 4-7 the first, 0x0c zero).
+                        const uint32_t p01 = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x0c0c0400u);
+                        const uint32_t p23 = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x0c0c0400u);
+                        res[b][g] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+                    } else if constexpr (OB == 2) {
+                        res[b][2 * g] = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u);
+                        res[b][2 * g + 1] = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            res[b][4 * g + i] = uint32_t(v[i]);
+                    }
+#pragma unroll
+                    for (int wd = 0; wd < OB; wd++)
+                        asm volatile("" : "+v"(res[b][g * OB + wd]));
+                    // Kept as a vector value (left alone, the compiler turns the
+                    // accumulation into compares and scalar ORs, a VALU -> SALU
+                    // dependency per value).
+                    if constexpr (RC)
+                        asm volatile("" : "+v"(bad_bits));
+                }
+            }
+            const int c0 = n0 + cl;
+#pragma unroll
+            for (int b = 0; b < TB; b++) {
+                if (m[b] < 0)
+                    continue;
+                const int64_t o = m[b] * E.N + c0;
+                uint8_t* dst = E.out + o * OB;
+                if (c0 + 16 <= E.N && ((o * OB) & 15) == 0) {
+#pragma unroll
+                    for (int wd = 0; wd < 4 * OB; wd += 4)
+                        *reinterpret_cast<v4u*>(dst + 4 * wd) =
+                            v4u{res[b][wd], res[b][wd + 1], res[b][wd + 2], res[b][wd + 3]};
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        res[b][4 * g + i] = uint32_t(v[i]);
-                }
-#pragma unroll
-                for (int wd = 0; wd < OB; wd++)
-                    asm volatile("" : "+v"(res[b][g * OB + wd]));
-                // Kept as a vector value (left alone, the compiler turns the
-                // accumulation into compares and scalar ORs, a VALU -> SALU
-                // dependency per value).
-                if constexpr (RS)
-                    asm volatile("" : "+v"(bad_bits));
-            }
-        }
-        const int c0 = n0 + cl;
-#pragma unroll
-        for (int b = 0; b < TB; b++) {
-            if (m[b] < 0)
-                continue;
-            const int64_t o = m[b] * E.N + c0;
-            uint8_t* dst = E.out + o * OB;
-            if (c0 + 16 <= E.N && ((o * OB) & 15) == 0) {
-#pragma unroll
-                for (int wd = 0; wd < 4 * OB; wd += 4)
-                    *reinterpret_cast<v4u*>(dst + 4 * wd) =
-                        v4u{res[b][wd], res[b][wd + 1], res[b][wd + 2], res[b][wd + 3]};
-            } else {
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    if (c0 + e >= E.N)
-                        continue;
-                    const uint32_t word = res[b][(e * OB) / 4];
-                    const int sh = 8 * ((e * OB) % 4);
-                    if constexpr (OB == 1)
-                        dst[e] = uint8_t(word >> sh);
-                    else if constexpr (OB == 2)
-                        reinterpret_cast<uint16_t*>(dst)[e] = uint16_t(word >> sh);
-                    else
-                        reinterpret_cast<uint32_t*>(dst)[e] = word;
+                    for (int e = 0; e < 16; e++) {
+                        if (c0 + e >= E.N)
+                            continue;
+                        const uint32_t word = res[b][(e * OB) / 4];
+                        const int sh = 8 * ((e * OB) % 4);
+                        if constexpr (OB == 1)
+                            dst[e] = uint8_t(word >> sh);
+                        else if constexpr (OB == 2)
+                            reinterpret_cast<uint16_t*>(dst)[e] = uint16_t(word >> sh);
+                        else
+                            reinterpret_cast<uint32_t*>(dst)[e] = word;
+                    }
                 }
             }
         }
-    }
+    };
+    if (E.range)
+        body(std::true_type{});
+    else
+        body(std::false_type{});
     if (bad_bits)
         atomicOr(E.err, DERR_SCALE_RANGE);
 }
@@ -1532,6 +1544,9 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
 // One wave per output channel:
 //   tab[2c]   = {bias + K zx zw - zx sum_k w[c][k] (mod 2^32), multiplier,
 //                -2^min(shift - 1, 31), shift}
+//               with the third word INT32_MIN instead when the channel's
+//               values cannot leave [-2^(shift-1), 2^(shift-1)):
+//               |bias| + max|x - zx| sum_k |w[c][k] - zw| < 2^(shift-1)
 //   tab[2c+1] = {rounding constant for values >= 0 (int64, lo/hi),
 //                rounding constant for values < 0 (int64, lo/hi)},
 //                both plus out_zp 2^shift
@@ -1552,9 +1567,13 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
         const int32_t zf = int32_t(uint32_t(uint8_t(zx)) * 0x01010101u);
         tab[2 * N] = v4i{zf, zf, zf, zf};
     }
+    // s: sum_k w; sa: sum_k |w - zw| (bytes biased by 128 to unsigned, which
+    // keeps differences, then v_sad_u8), the latter only with a RESCALE.
     int32_t s = 0;
-    if (zx != 0) {
+    uint32_t sa = 0;
+    if (zx != 0 || mult) {
         const int8_t* wr = w + int64_t(c) * cstride;
+        const uint32_t zwb = (uint32_t(uint8_t(zw)) * 0x01010101u) ^ 0x80808080u;
         if (kstride == 1 && K % 16 == 0 && reinterpret_cast<uintptr_t>(wr) % 16 == 0) {
             // Contiguous rows: 16 bytes per lane per step, summed with dot4.
             for (int k = 16 * lane; k < K; k += 16 * 64) {
@@ -1563,14 +1582,25 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
                 s = __builtin_amdgcn_sdot4(int(v.y), 0x01010101, s, false);
                 s = __builtin_amdgcn_sdot4(int(v.z), 0x01010101, s, false);
                 s = __builtin_amdgcn_sdot4(int(v.w), 0x01010101, s, false);
+                sa = __builtin_amdgcn_sad_u8(v.x ^ 0x80808080u, zwb, sa);
+                sa = __builtin_amdgcn_sad_u8(v.y ^ 0x80808080u, zwb, sa);
+                sa = __builtin_amdgcn_sad_u8(v.z ^ 0x80808080u, zwb, sa);
+                sa = __builtin_amdgcn_sad_u8(v.w ^ 0x80808080u, zwb, sa);
             }
         } else {
-            for (int k = lane; k < K; k += 64)
-                s += wr[int64_t(k) * kstride];
+            for (int k = lane; k < K; k += 64) {
+                const int32_t v = wr[int64_t(k) * kstride];
+                s += v;
+                sa += uint32_t(v > zw ? v - zw : zw - v);
+            }
         }
     }
-    for (int off = 32; off > 0; off >>= 1)
+    // Lane sums stay below 2^32 for K < 2^24 / 255 per lane.
+    uint64_t sa64 = sa;
+    for (int off = 32; off > 0; off >>= 1) {
         s += __shfl_xor(s, off);
+        sa64 += __shfl_xor(sa64, off);
+    }
     if (lane != 0)
         return;
     uint32_t add = bias ? uint32_t(bias[bias_len == 1 ? 0 : c]) : 0u;
@@ -1590,7 +1620,14 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
     const int64_t rp = half + d + zps, rn = half - d + zps;
     // Range bound of apply_scale_32's REQUIRE: values in [lo, ~lo] with
     // lo = -2^min(s - 1, 31).
-    const int32_t lo = sh - 1 < 31 ? -(int32_t(1) << (sh - 1)) : INT32_MIN;
+    int32_t lo = sh - 1 < 31 ? -(int32_t(1) << (sh - 1)) : INT32_MIN;
+    if (mult && lo != INT32_MIN) {
+        const int64_t b = bias ? int64_t(bias[bias_len == 1 ? 0 : c]) : 0;
+        const int64_t xmax = std::max<int64_t>(128 + int64_t(zx), 127 - int64_t(zx));
+        const uint64_t bound = uint64_t(b < 0 ? -b : b) + sa64 * uint64_t(xmax);
+        if (K < (1 << 24) && bound < (uint64_t(1) << (sh - 1)))  // K bound: no lane sum overflow
+            lo = INT32_MIN;
+    }
     tab[2 * c] = v4i{int32_t(add), m, lo, sh};
     reinterpret_cast<int32_t*>(tab + 2 * N + 1)[c] = int32_t(add);
     tab[2 * c + 1] = v4i{int32_t(uint32_t(uint64_t(rp))), int32_t(uint64_t(rp) >> 32),
@@ -1947,6 +1984,21 @@ void conv_i8_table(const ConvI8Desc& d, const RescaleDev* rs, void* tab, hipStre
                        int32_t(conv_i8_table_stride(d.oc) / 4));
 }
 
+bool conv_i8_table_range_safe(const ConvI8Desc& d, const void* tab)
+{
+    if (d.oc <= 0)
+        return true;
+    const int batch = d.depthwise ? 1 : d.batch;
+    std::vector<int32_t> h(size_t(conv_i8_table_words(d.oc, batch)));
+    hip_check(hipMemcpy(h.data(), tab, h.size() * sizeof(int32_t), hipMemcpyDeviceToHost), "conv_i8 table readback");
+    const int64_t stride = conv_i8_table_stride(d.oc);
+    for (int b = 0; b < batch; b++)
+        for (int c = 0; c < d.oc; c++)
+            if (h[size_t(b * stride + int64_t(CONV_I8_TABLE_WORDS) * c + 2)] != INT32_MIN)
+                return false;
+    return true;
+}
+
 int32_t conv_i8_im2col_kp(const ConvI8Desc& d) { return (d.kh * d.kw * d.ic + 15) / 16 * 16; }
 
 void conv_i8_im2col(const ConvI8Desc& d, int8_t* xcol, hipStream_t stream)
@@ -2068,7 +2120,7 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
         // [lo, hi] (prepare_clamp_int decodes them in that type).
         e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
         e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
-        e.range = rs->min_shift <= 31;
+        e.range = rs->min_shift <= 31 && !d.range_safe;
         ob = rs->out_bytes;
     }
     if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)

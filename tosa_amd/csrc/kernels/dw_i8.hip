@@ -300,7 +300,7 @@ bool depthwise_i8_lds(const ConvI8Desc& d, const void* tab, const RescaleDev* rs
     if (rs) {
         a.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
         a.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
-        a.range = rs->min_shift <= 31;
+        a.range = rs->min_shift <= 31 && !d.range_safe;
         ob = rs->out_bytes;
     }
     // The workgroup owns every channel of its pixels: coalesced staging,

@@ -240,6 +240,10 @@ StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* b
     conv_i8_table(d, rs, t->device_out(), s);
     if (cacheable) {
         hip_check(hipStreamSynchronize(s), "conv_i8 table");
+        // A cached table is read back once: when it rules out every range
+        // failure, the kernels drop the per-value check.
+        if (rs && rs->min_shift <= 31)
+            t->scale_range_safe = conv_i8_table_range_safe(d, t->device_in());
         std::lock_guard<std::mutex> lk(derived_mu());
         wstore.derived[key] = t;
     }
@@ -892,6 +896,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
                 auto wp = conv_i8_wpack_for(fd, *weight->data, w_const, s);
                 ConvI8Desc f = fd;
                 f.wpack = wp ? static_cast<const int8_t*>(wp->device_in()) : nullptr;
+                f.range_safe = tab->scale_range_safe;
                 conv_i8_fast(f, tab->device_in(), rs, out, err, s);
                 return;
             }
@@ -917,6 +922,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
                 p.pt = p.pl = 0;
                 p.sy = p.sx = p.dy = p.dx = 1;
                 p.wpack = nullptr;
+                p.range_safe = tab->scale_range_safe;
                 conv_i8_fast(p, tab->device_in(), rs, out, err, s);
                 return;
             }
@@ -1162,6 +1168,7 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
             });
             d.w = static_cast<const int8_t*>(bt->device_in());
             auto tab = conv_i8_table_for(d, *b->data, nullptr, rs, b_const && (!rs || rs_const), s);
+            d.range_safe = tab->scale_range_safe;
             conv_i8_fast(d, tab->device_in(), rs, out, err, s);
         };
         if (auto tail = plan_tail(st, index, out_shape)) {

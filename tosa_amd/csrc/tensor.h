@@ -42,6 +42,11 @@ struct Storage {
     std::vector<uint8_t> host;
     bool host_valid = false;
 
+    // An int8 convolution's epilogue table that rules out every failure of
+    // apply_scale_32's range REQUIRE (set once the table is known on the
+    // host; false, i.e. check it, otherwise).
+    bool scale_range_safe = false;
+
     // Virtual storage: fills this storage (device side) when first read.
     std::function<void(Storage&)> materialize;
 
