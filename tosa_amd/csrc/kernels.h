@@ -136,6 +136,8 @@ bool conv_i8_table_range_safe(const ConvI8Desc& d, const void* tab);
 // Bytes of the packed weight layout of the stride-1 halo kernel for `d`, 0
 // when that kernel does not run for `d`; conv_i8_wpack writes it from d.w.
 int64_t conv_i8_wpack_bytes(const ConvI8Desc& d);
+// Output channels per block of that layout (0 when it does not apply).
+int conv_i8_wpack_block(const ConvI8Desc& d);
 void conv_i8_wpack(const ConvI8Desc& d, void* wp, hipStream_t stream);
 // Convolutions that conv_i8_fast_supported rejects only for their channel
 // alignment or geometry run as a pointwise GEMM over a materialised im2col:

@@ -770,14 +770,17 @@ struct Halo32Args {
     const v4i* tab;    // [N][2] entries, 16 bytes of the input zero point, [N] additive constants
     int32_t N, IC, IH, IW, OH, OW, KW, taps, dy, dx, pt, pl;
     int32_t R, tiles_per_img, HR, HW;
+    int32_t PG;      // waves along the pixels (4 or 8): the launch's template
     int32_t sbytes;  // LDS bytes of one halo stage (HR*HW*64, 1 KB multiple)
     int32_t wbytes;  // bytes of one pass's weights (taps * BC * 32)
     FastDiv div_ow, div_hw;
     EpiArgs E;
 };
 
-constexpr int H32_TB = 2;                // 32-pixel tiles per wave
-constexpr int H32_BP = 4 * 32 * H32_TB;  // pixel slots per workgroup
+constexpr int H32_TB = 2;  // 32-pixel tiles per wave
+// Pixel slots of a workgroup with PG waves along the pixels.
+constexpr int h32_bp(int pg) { return pg * 32 * H32_TB; }
+constexpr int H32_BP_MAX = h32_bp(8);
 
 // A direct 16-byte global->LDS load (global_load_lds_dwordx4: lane l writes
 // LDS byte address `l` + 16 l, `l` wave-uniform). Issued through inline
@@ -797,9 +800,9 @@ __device__ __forceinline__ int h32_row_channel(int r) { return 16 * ((r >> 2) & 
 
 // Epilogue of the 32x32 layout: lane (h, l32) holds channels 32 a + 16 h +
 // 0..15 (counted from n0; s_tab starts at channel n0) of tile pixel
-// 32 (pw + 4 b) + l32 in acc[a][b], the channel's additive constant already
+// 32 (pw + PG b) + l32 in acc[a][b], the channel's additive constant already
 // included.
-template <int TA, int TB, int OB, bool RS, bool ZW, typename PixelMap>
+template <int TA, int TB, int PG, int OB, bool RS, bool ZW, typename PixelMap>
 __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab, const int32_t* s_rowsum, int n0,
                                            int pw, int lane, const EpiArgs& E, PixelMap pixel)
 {
@@ -811,7 +814,7 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
     int64_t m[TB];
 #pragma unroll
     for (int b = 0; b < TB; b++) {
-        const int p = 32 * (pw + 4 * b) + l32;
+        const int p = 32 * (pw + PG * b) + l32;
         m[b] = pixel(p);
         zwx[b] = 0;
         if constexpr (ZW)
@@ -937,13 +940,15 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
 
 // KT: taps when fixed at compile time (9 = 3x3; the tap loop is then fully
 // unrolled so that each tap waits only for its own fragments), 0 = any.
-template <int BC, int KT, int OB, bool RS, bool ZW>
-__global__ void __launch_bounds__(BC * 4, 2) conv_i8_halo32_kernel(Halo32Args A)
+// PG: waves along the pixels (each wave takes 64 channels), so BC / 64 * PG
+// waves in all.
+template <int BC, int PG, int KT, int OB, bool RS, bool ZW>
+__global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Halo32Args A)
 {
-    constexpr int NT = BC * 4;  // threads: 4 waves per 64 channels
-    constexpr int TA = 2;       // 32-channel tiles per wave
-    constexpr int TB = H32_TB;  // 32-pixel tiles per wave
-    constexpr int BP = H32_BP;
+    constexpr int NT = BC / 64 * PG * 64;  // threads
+    constexpr int TA = 2;                  // 32-channel tiles per wave
+    constexpr int TB = H32_TB;             // 32-pixel tiles per wave
+    constexpr int BP = h32_bp(PG);
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* const halo = smem;                                          // [2][sbytes]
@@ -955,8 +960,8 @@ __global__ void __launch_bounds__(BC * 4, 2) conv_i8_halo32_kernel(Halo32Args A)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int pw = wave & 3;        // pixel tiles pw, pw + 4
-    const int cw = 64 * (wave >> 2);  // first channel of the wave (tile-relative)
+    const int pw = wave % PG;         // pixel tiles pw, pw + PG
+    const int cw = 64 * (wave / PG);  // first channel of the wave (tile-relative)
     const int l32 = lane & 31;
     const int h = lane >> 5;
     // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2);
@@ -1012,7 +1017,7 @@ __global__ void __launch_bounds__(BC * 4, 2) conv_i8_halo32_kernel(Halo32Args A)
     int32_t hpos[TB];
 #pragma unroll
     for (int b = 0; b < TB; b++) {
-        const int p = 32 * (pw + 4 * b) + l32;
+        const int p = 32 * (pw + PG * b) + l32;
         const int pp = p < npix ? p : 0;
         const int r = fdiv(pp, A.div_ow);
         hpos[b] = r * A.HW + pp - r * A.OW;
@@ -1171,7 +1176,7 @@ __global__ void __launch_bounds__(BC * 4, 2) conv_i8_halo32_kernel(Halo32Args A)
     }
 
     const int m0 = (img * A.OH + oy0) * A.OW;
-    epilogue32<TA, TB, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
+    epilogue32<TA, TB, PG, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
                                    [&](int p) { return p < npix ? m0 + p : -1; });
 }
 
@@ -1796,10 +1801,10 @@ bool halo_plan(const ConvI8Desc& d, bool zw, HaloArgs& a, int& bc, int& kc, size
     return true;
 }
 
-template <int BC, int KT, int OB, bool RS, bool ZW>
+template <int BC, int PG, int KT, int OB, bool RS, bool ZW>
 void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t s)
 {
-    auto kfn = conv_i8_halo32_kernel<BC, KT, OB, RS, ZW>;
+    auto kfn = conv_i8_halo32_kernel<BC, PG, KT, OB, RS, ZW>;
     static bool attr = [&]() {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       HALO_LDS_MAX),
@@ -1807,24 +1812,24 @@ void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL(kfn, dim3(blocks, (a.N + BC - 1) / BC), dim3(BC * 4), lds, s, a);
+    hipLaunchKernelGGL(kfn, dim3(blocks, (a.N + BC - 1) / BC), dim3(BC / 64 * PG * 64), lds, s, a);
 }
 
-template <int BC, int KT>
+template <int BC, int PG, int KT>
 void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob, bool rs, bool zw, hipStream_t s)
 {
     if (!rs) {
         if (zw)
-            launch_halo32<BC, KT, 4, false, true>(a, blocks, lds, s);
+            launch_halo32<BC, PG, KT, 4, false, true>(a, blocks, lds, s);
         else
-            launch_halo32<BC, KT, 4, false, false>(a, blocks, lds, s);
+            launch_halo32<BC, PG, KT, 4, false, false>(a, blocks, lds, s);
         return;
     }
-#define TOSA_HALO32_OB(OBV)                                       \
-    if (zw)                                                       \
-        launch_halo32<BC, KT, OBV, true, true>(a, blocks, lds, s); \
-    else                                                          \
-        launch_halo32<BC, KT, OBV, true, false>(a, blocks, lds, s);
+#define TOSA_HALO32_OB(OBV)                                           \
+    if (zw)                                                           \
+        launch_halo32<BC, PG, KT, OBV, true, true>(a, blocks, lds, s); \
+    else                                                              \
+        launch_halo32<BC, PG, KT, OBV, true, false>(a, blocks, lds, s);
     if (ob == 1) {
         TOSA_HALO32_OB(1)
     } else if (ob == 2) {
@@ -1853,42 +1858,58 @@ int cu_count()
 }
 
 // Geometry of the 32x32 halo kernel for `d`, or false when it does not
-// apply: stride 1, ic a multiple of 32, output rows of at most 256 pixels,
-// tiles of at least 96 pixels and buffers within the LDS. The rows per tile
-// R minimise (workgroup rounds, one workgroup per CU) x (pixel tiles of the
-// busiest wave + 1), the 1 standing for a tile's fixed cost (first loads,
-// epilogue).
+// apply: stride 1, ic a multiple of 32, output rows of at most 512 pixels,
+// tiles of at least 96 pixels and buffers within the LDS. Layouts: 128
+// channels x 4 waves along the pixels, or 64 channels x 8 or 4 waves. The
+// layout and rows per tile R minimise (workgroup rounds, one workgroup per
+// CU) x (pixel tiles of the busiest wave + 1), the 1 standing for a tile's
+// fixed cost (first loads, epilogue); ties go to the fewest bytes loaded per
+// CU (weights + halo: 64-channel tiles over twice the pixels load half the
+// weights per tile, and the loads' issue holds up the waves that make them).
 bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& lds, unsigned& blocks)
 {
-    if (d.sy != 1 || d.sx != 1 || d.ic % 32 != 0 || d.ow > H32_BP || d.oh < 1 || d.ow < 1 || d.depthwise)
+    if (d.sy != 1 || d.sx != 1 || d.ic % 32 != 0 || d.ow > H32_BP_MAX || d.oh < 1 || d.ow < 1 || d.depthwise)
         return false;
-    bc = d.oc > 64 ? 128 : 64;
     const int taps = d.kh * d.kw;
     const int HW = d.ow + (d.kw - 1) * d.dx;
-    auto lds_for = [&](int R) {
+    auto lds_for = [&](int R, int c, int pg) {
         const size_t hw = (size_t(R) + size_t(d.kh - 1) * d.dy) * HW;
-        size_t b = 2 * ((hw * 64 + 1023) / 1024 * 1024) + 2 * size_t(taps) * bc * 32 + size_t(32) * bc;
+        size_t b = 2 * ((hw * 64 + 1023) / 1024 * 1024) + 2 * size_t(taps) * c * 32 + size_t(32) * c;
         if (zw)
-            b += size_t(4) * (hw + H32_BP);
+            b += size_t(4) * (hw + h32_bp(pg));
         return b;
     };
-    const int rmax = d.oh < H32_BP / d.ow ? d.oh : H32_BP / d.ow;
-    const long chb = (d.oc + bc - 1) / bc;
     const long cus = cu_count();
-    int R = 0;
-    long best = 0;
-    for (int r = rmax; r >= 1; r--) {
-        if (r * d.ow < 96 && r != d.oh)
-            break;
-        if (lds_for(r) > size_t(HALO_LDS_MAX))
+    int R = 0, PG = 0;
+    bc = 0;
+    long best = 0, best_bytes = 0;
+    const int layouts[3][2] = {{128, 4}, {64, 8}, {64, 4}};
+    for (const auto& lay : layouts) {
+        const int c = lay[0], pg = lay[1];
+        if (c == 128 && d.oc <= 64)
             continue;
-        const long tiles = (r * d.ow + 31) / 32;
-        const long per_wave = (tiles + 3) / 4;
-        const long nb = long(d.n) * ((d.oh + r - 1) / r) * chb;
-        const long cost = (nb + cus - 1) / cus * (per_wave + 1);
-        if (R == 0 || cost < best) {
-            R = r;
-            best = cost;
+        if (d.ow > h32_bp(pg))
+            continue;
+        const int rmax = d.oh < h32_bp(pg) / d.ow ? d.oh : h32_bp(pg) / d.ow;
+        const long chb = (d.oc + c - 1) / c;
+        for (int r = rmax; r >= 1; r--) {
+            if (r * d.ow < 96 && r != d.oh)
+                break;
+            if (lds_for(r, c, pg) > size_t(HALO_LDS_MAX))
+                continue;
+            const long tiles = (r * d.ow + 31) / 32;
+            const long per_wave = (tiles + pg - 1) / pg;
+            const long nb = long(d.n) * ((d.oh + r - 1) / r) * chb;
+            const long rounds = (nb + cus - 1) / cus;
+            const long cost = rounds * (per_wave + 1);
+            const long bytes = rounds * (long(taps) * c * d.ic + (long(r) + long(d.kh - 1) * d.dy) * HW * d.ic);
+            if (R == 0 || cost < best || (cost == best && bytes < best_bytes)) {
+                R = r;
+                PG = pg;
+                bc = c;
+                best = cost;
+                best_bytes = bytes;
+            }
         }
     }
     if (R == 0 || R * d.ow < 96)
@@ -1913,9 +1934,10 @@ bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& l
     a.HW = HW;
     a.sbytes = int32_t((size_t(a.HR) * HW * 64 + 1023) / 1024 * 1024);
     a.wbytes = taps * bc * 32;
+    a.PG = PG;
     a.div_ow = FastDiv(uint32_t(d.ow));
     a.div_hw = FastDiv(uint32_t(HW));
-    lds = lds_for(R);
+    lds = lds_for(R, bc, PG);
     blocks = unsigned(d.n) * unsigned(a.tiles_per_img);
     return true;
 }
@@ -2069,7 +2091,9 @@ void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t
         hipLaunchKernelGGL(transpose_b_kernel<false>, grid, dim3(256), 0, stream, b, c, w, out);
 }
 
-int64_t conv_i8_wpack_bytes(const ConvI8Desc& d)
+// Channel block of the packed weights (the halo kernel's workgroup
+// channels), 0 when the halo kernel does not run for `d`.
+int conv_i8_wpack_block(const ConvI8Desc& d)
 {
     Halo32Args a{};
     int bc = 0;
@@ -2079,6 +2103,14 @@ int64_t conv_i8_wpack_bytes(const ConvI8Desc& d)
                     d.iw == d.ow;
     if (pw || !conv_i8_fast_supported(d) || !halo32_plan(d, d.zp_w != 0, a, bc, lds, blocks))
         return 0;
+    return bc;
+}
+
+int64_t conv_i8_wpack_bytes(const ConvI8Desc& d)
+{
+    const int bc = conv_i8_wpack_block(d);
+    if (bc == 0)
+        return 0;
     return int64_t((d.oc + bc - 1) / bc) * bc * d.kh * d.kw * d.ic;
 }
 
@@ -2087,7 +2119,7 @@ void conv_i8_wpack(const ConvI8Desc& d, void* wp, hipStream_t stream)
     const int64_t bytes = conv_i8_wpack_bytes(d);
     if (bytes <= 0)
         return;
-    const int bc = d.oc > 64 ? 128 : 64;
+    const int bc = conv_i8_wpack_block(d);
     const int64_t slots = bytes / 16;
     hipLaunchKernelGGL(conv_i8_wpack_kernel, dim3(unsigned((slots + 255) / 256)), dim3(256), 0, stream, d.w, d.oc,
                        d.kh * d.kw * d.ic, d.ic, d.kh * d.kw, bc, slots, static_cast<v4u*>(wp));
@@ -2173,14 +2205,19 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
         const bool k3 = d.kh == 3 && d.kw == 3;
         if (bc == 128) {
             if (k3)
-                launch_halo32_epi<128, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<128, 4, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
             else
-                launch_halo32_epi<128, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<128, 4, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+        } else if (h32.PG == 8) {
+            if (k3)
+                launch_halo32_epi<64, 8, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+            else
+                launch_halo32_epi<64, 8, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
         } else {
             if (k3)
-                launch_halo32_epi<64, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<64, 4, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
             else
-                launch_halo32_epi<64, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<64, 4, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
         }
         return;
     }

@@ -258,7 +258,7 @@ StoragePtr conv_i8_wpack_for(const ConvI8Desc& d, Storage& wstore, bool cacheabl
     const int64_t bytes = conv_i8_wpack_bytes(d);
     if (bytes <= 0)
         return nullptr;
-    const std::string key = "conv_i8_wpack:" + std::to_string(bytes);
+    const std::string key = "conv_i8_wpack:" + std::to_string(bytes) + ":" + std::to_string(conv_i8_wpack_block(d));
     if (cacheable) {
         std::lock_guard<std::mutex> lk(derived_mu());
         auto it = wstore.derived.find(key);
