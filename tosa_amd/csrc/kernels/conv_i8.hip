@@ -770,17 +770,17 @@ struct Halo32Args {
     const v4i* tab;    // [N][2] entries, 16 bytes of the input zero point, [N] additive constants
     int32_t N, IC, IH, IW, OH, OW, KW, taps, dy, dx, pt, pl;
     int32_t R, tiles_per_img, HR, HW;
-    int32_t PG;      // waves along the pixels (4 or 8): the launch's template
+    int32_t PG, TB;  // waves along the pixels, 32-pixel tiles per wave: the launch's template
     int32_t sbytes;  // LDS bytes of one halo stage (HR*HW*64, 1 KB multiple)
     int32_t wbytes;  // bytes of one pass's weights (taps * BC * 32)
     FastDiv div_ow, div_hw;
     EpiArgs E;
 };
 
-constexpr int H32_TB = 2;  // 32-pixel tiles per wave
-// Pixel slots of a workgroup with PG waves along the pixels.
-constexpr int h32_bp(int pg) { return pg * 32 * H32_TB; }
-constexpr int H32_BP_MAX = h32_bp(8);
+// Pixel slots of a workgroup with PG waves along the pixels, TB 32-pixel
+// tiles each.
+constexpr int h32_bp(int pg, int tb) { return pg * 32 * tb; }
+constexpr int H32_BP_MAX = h32_bp(8, 2);
 
 // A direct 16-byte global->LDS load (global_load_lds_dwordx4: lane l writes
 // LDS byte address `l` + 16 l, `l` wave-uniform). Issued through inline
@@ -941,14 +941,13 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
 // KT: taps when fixed at compile time (9 = 3x3; the tap loop is then fully
 // unrolled so that each tap waits only for its own fragments), 0 = any.
 // PG: waves along the pixels (each wave takes 64 channels), so BC / 64 * PG
-// waves in all.
-template <int BC, int PG, int KT, int OB, bool RS, bool ZW>
+// waves in all; TB: 32-pixel tiles per wave.
+template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW>
 __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Halo32Args A)
 {
     constexpr int NT = BC / 64 * PG * 64;  // threads
     constexpr int TA = 2;                  // 32-channel tiles per wave
-    constexpr int TB = H32_TB;             // 32-pixel tiles per wave
-    constexpr int BP = h32_bp(PG);
+    constexpr int BP = h32_bp(PG, TB);
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* const halo = smem;                                          // [2][sbytes]
@@ -959,8 +958,8 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int pw = wave % PG;         // pixel tiles pw, pw + PG
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pw = wave % PG;         // pixel tiles pw, pw + PG, ..
     const int cw = 64 * (wave / PG);  // first channel of the wave (tile-relative)
     const int l32 = lane & 31;
     const int h = lane >> 5;
@@ -1013,7 +1012,11 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     }
 
     // Halo position (tap 0) of this lane's pixel in each tile; pixels past
-    // the tile's end read pixel 0 and are not stored.
+    // the tile's end read pixel 0 and are not stored. With one tile per wave
+    // (the layout for short tiles), a wave whose tile holds no pixel skips
+    // its MFMAs and epilogue; its loads and barriers stay. (The branch costs
+    // the two-tile layouts' tap loop more than the idle waves would save.)
+    const bool live = TB > 1 || 32 * pw < npix;
     int32_t hpos[TB];
 #pragma unroll
     for (int b = 0; b < TB; b++) {
@@ -1114,7 +1117,9 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
                 for (int a = 0; a < TA; a++)
                     acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], acc[a][b], 0, 0, 0);
         };
-        if constexpr (KT == 9) {
+        if (!live) {
+            // no pixels: only the loads and barriers of the pass
+        } else if constexpr (KT == 9) {
             v4i fa[2][TA], fb[2][TB];
             load(fa[0], fb[0], 0, 0, 0);
 #pragma unroll
@@ -1176,8 +1181,9 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     }
 
     const int m0 = (img * A.OH + oy0) * A.OW;
-    epilogue32<TA, TB, PG, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
-                                   [&](int p) { return p < npix ? m0 + p : -1; });
+    if (live)
+        epilogue32<TA, TB, PG, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
+                                       [&](int p) { return p < npix ? m0 + p : -1; });
 }
 
 // Packed weights of the 32x32 halo kernel: 16-byte slot
@@ -1801,10 +1807,10 @@ bool halo_plan(const ConvI8Desc& d, bool zw, HaloArgs& a, int& bc, int& kc, size
     return true;
 }
 
-template <int BC, int PG, int KT, int OB, bool RS, bool ZW>
+template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW>
 void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t s)
 {
-    auto kfn = conv_i8_halo32_kernel<BC, PG, KT, OB, RS, ZW>;
+    auto kfn = conv_i8_halo32_kernel<BC, PG, TB, KT, OB, RS, ZW>;
     static bool attr = [&]() {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       HALO_LDS_MAX),
@@ -1815,21 +1821,21 @@ void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t
     hipLaunchKernelGGL(kfn, dim3(blocks, (a.N + BC - 1) / BC), dim3(BC / 64 * PG * 64), lds, s, a);
 }
 
-template <int BC, int PG, int KT>
+template <int BC, int PG, int TB, int KT>
 void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob, bool rs, bool zw, hipStream_t s)
 {
     if (!rs) {
         if (zw)
-            launch_halo32<BC, PG, KT, 4, false, true>(a, blocks, lds, s);
+            launch_halo32<BC, PG, TB, KT, 4, false, true>(a, blocks, lds, s);
         else
-            launch_halo32<BC, PG, KT, 4, false, false>(a, blocks, lds, s);
+            launch_halo32<BC, PG, TB, KT, 4, false, false>(a, blocks, lds, s);
         return;
     }
-#define TOSA_HALO32_OB(OBV)                                           \
-    if (zw)                                                           \
-        launch_halo32<BC, PG, KT, OBV, true, true>(a, blocks, lds, s); \
-    else                                                              \
-        launch_halo32<BC, PG, KT, OBV, true, false>(a, blocks, lds, s);
+#define TOSA_HALO32_OB(OBV)                                               \
+    if (zw)                                                               \
+        launch_halo32<BC, PG, TB, KT, OBV, true, true>(a, blocks, lds, s); \
+    else                                                                  \
+        launch_halo32<BC, PG, TB, KT, OBV, true, false>(a, blocks, lds, s);
     if (ob == 1) {
         TOSA_HALO32_OB(1)
     } else if (ob == 2) {
@@ -1859,53 +1865,60 @@ int cu_count()
 
 // Geometry of the 32x32 halo kernel for `d`, or false when it does not
 // apply: stride 1, ic a multiple of 32, output rows of at most 512 pixels,
-// tiles of at least 96 pixels and buffers within the LDS. Layouts: 128
-// channels x 4 waves along the pixels, or 64 channels x 8 or 4 waves. The
+// tiles of at least 96 pixels and buffers within the LDS. Layouts (output
+// channels x waves along the pixels x 32-pixel tiles per wave): 128 x 4 x 2,
+// 64 x 8 x 2 and 64 x 8 x 1. Wave w sits on SIMD w % 4 and computes all
+// its tiles when its first one holds pixels (none otherwise), so the
+// busiest SIMD's MFMA work is the largest sum of its live waves' tiles. The
 // layout and rows per tile R minimise (workgroup rounds, one workgroup per
-// CU) x (pixel tiles of the busiest wave + 1), the 1 standing for a tile's
-// fixed cost (first loads, epilogue); ties go to the fewest bytes loaded per
-// CU (weights + halo: 64-channel tiles over twice the pixels load half the
-// weights per tile, and the loads' issue holds up the waves that make them).
+// CU) x (that sum + 2), the 2 standing for a tile's fixed cost (first
+// loads, epilogue); ties go to the fewest bytes loaded per CU (weights +
+// halo: the loads' issue holds up the waves that make them).
 bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& lds, unsigned& blocks)
 {
     if (d.sy != 1 || d.sx != 1 || d.ic % 32 != 0 || d.ow > H32_BP_MAX || d.oh < 1 || d.ow < 1 || d.depthwise)
         return false;
     const int taps = d.kh * d.kw;
     const int HW = d.ow + (d.kw - 1) * d.dx;
-    auto lds_for = [&](int R, int c, int pg) {
+    auto lds_for = [&](int R, int c, int bp) {
         const size_t hw = (size_t(R) + size_t(d.kh - 1) * d.dy) * HW;
         size_t b = 2 * ((hw * 64 + 1023) / 1024 * 1024) + 2 * size_t(taps) * c * 32 + size_t(32) * c;
         if (zw)
-            b += size_t(4) * (hw + h32_bp(pg));
+            b += size_t(4) * (hw + bp);
         return b;
     };
     const long cus = cu_count();
-    int R = 0, PG = 0;
+    int R = 0, PG = 0, TB = 0;
     bc = 0;
     long best = 0, best_bytes = 0;
-    const int layouts[3][2] = {{128, 4}, {64, 8}, {64, 4}};
+    const int layouts[3][3] = {{128, 4, 2}, {64, 8, 2}, {64, 8, 1}};
     for (const auto& lay : layouts) {
-        const int c = lay[0], pg = lay[1];
-        if (c == 128 && d.oc <= 64)
+        const int c = lay[0], pg = lay[1], tb = lay[2], bp = h32_bp(pg, tb);
+        if ((c == 128 && d.oc <= 64) || d.ow > bp)
             continue;
-        if (d.ow > h32_bp(pg))
-            continue;
-        const int rmax = d.oh < h32_bp(pg) / d.ow ? d.oh : h32_bp(pg) / d.ow;
+        const int rmax = d.oh < bp / d.ow ? d.oh : bp / d.ow;
         const long chb = (d.oc + c - 1) / c;
         for (int r = rmax; r >= 1; r--) {
             if (r * d.ow < 96 && r != d.oh)
                 break;
-            if (lds_for(r, c, pg) > size_t(HALO_LDS_MAX))
+            if (lds_for(r, c, bp) > size_t(HALO_LDS_MAX))
                 continue;
-            const long tiles = (r * d.ow + 31) / 32;
-            const long per_wave = (tiles + pg - 1) / pg;
+            const int tiles = (r * d.ow + 31) / 32;
+            long simd_max = 0;
+            for (int sm = 0; sm < 4; sm++) {
+                long t = 0;
+                for (int w = sm; w < c / 64 * pg; w += 4)
+                    t += (w % pg) < tiles ? tb : 0;
+                simd_max = t > simd_max ? t : simd_max;
+            }
             const long nb = long(d.n) * ((d.oh + r - 1) / r) * chb;
             const long rounds = (nb + cus - 1) / cus;
-            const long cost = rounds * (per_wave + 1);
+            const long cost = rounds * (simd_max + 2);
             const long bytes = rounds * (long(taps) * c * d.ic + (long(r) + long(d.kh - 1) * d.dy) * HW * d.ic);
             if (R == 0 || cost < best || (cost == best && bytes < best_bytes)) {
                 R = r;
                 PG = pg;
+                TB = tb;
                 bc = c;
                 best = cost;
                 best_bytes = bytes;
@@ -1935,9 +1948,10 @@ bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& l
     a.sbytes = int32_t((size_t(a.HR) * HW * 64 + 1023) / 1024 * 1024);
     a.wbytes = taps * bc * 32;
     a.PG = PG;
+    a.TB = TB;
     a.div_ow = FastDiv(uint32_t(d.ow));
     a.div_hw = FastDiv(uint32_t(HW));
-    lds = lds_for(R, bc, PG);
+    lds = lds_for(R, bc, h32_bp(PG, TB));
     blocks = unsigned(d.n) * unsigned(a.tiles_per_img);
     return true;
 }
@@ -2205,19 +2219,19 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
         const bool k3 = d.kh == 3 && d.kw == 3;
         if (bc == 128) {
             if (k3)
-                launch_halo32_epi<128, 4, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<128, 4, 2, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
             else
-                launch_halo32_epi<128, 4, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
-        } else if (h32.PG == 8) {
+                launch_halo32_epi<128, 4, 2, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+        } else if (h32.TB == 2) {
             if (k3)
-                launch_halo32_epi<64, 8, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<64, 8, 2, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
             else
-                launch_halo32_epi<64, 8, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<64, 8, 2, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
         } else {
             if (k3)
-                launch_halo32_epi<64, 4, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<64, 8, 1, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
             else
-                launch_halo32_epi<64, 4, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+                launch_halo32_epi<64, 8, 1, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
         }
         return;
     }
