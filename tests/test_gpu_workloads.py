@@ -511,3 +511,62 @@ def test_gemm_f16_conv1x1(dtype, out_dtype, shape):
     u = {"FP32": 0.0, "BF16": 2.0 ** -8, "FP16": 2.0 ** -11}[out_dtype]
     bound = 2 * cin * 2.0 ** -24 * absy + 2.0 ** -24 * np.abs(exact) + 2 * u * (np.abs(acc) + np.abs(exact)) + 1e-30
     assert np.all(np.abs(got - exact) <= bound), np.abs(got - exact).max()
+
+
+# Stride-1 bf16/fp16 convolutions on the halo kernel's float variant: 3x3 and
+# other taps, padding, dilation, ragged output channels, and fp32 / bf16 /
+# fp16 outputs. The small shapes take the 64-channel one-tile layout, the
+# last one the 128-channel layout; the cfg5 workload test above takes the
+# 64-channel two-tile layout.
+FLOAT_HALO = [
+    # n, h, w, cin, cout, kh, kw, pad, dil
+    (2, 28, 28, 128, 128, 3, 3, (1, 1, 1, 1), (1, 1)),
+    (1, 14, 14, 256, 200, 3, 3, (1, 1, 1, 1), (1, 1)),
+    (2, 20, 30, 64, 96, 5, 5, (2, 2, 2, 2), (1, 1)),
+    (1, 16, 40, 48, 40, 1, 3, (0, 0, 1, 1), (1, 1)),
+    (3, 12, 12, 32, 64, 3, 3, (2, 2, 2, 2), (2, 2)),
+    (1, 9, 61, 16, 136, 2, 2, (0, 1, 1, 0), (1, 1)),
+    (43, 4, 4, 16, 384, 3, 3, (1, 1, 1, 1), (1, 1)),
+]
+
+
+@pytest.mark.parametrize("dtype,out_dtype", [("BF16", "FP32"), ("FP16", "FP32"), ("BF16", "BF16"), ("FP16", "FP16")])
+@pytest.mark.parametrize("case", range(len(FLOAT_HALO)))
+def test_float_halo_conv(dtype, out_dtype, case):
+    import torch
+    n, h, w_, cin, cout, kh, kw, pad, dil = FLOAT_HALO[case]
+    r = np.random.default_rng(8100 + 10 * case + len(dtype) + len(out_dtype))
+    oh = h - 1 + pad[0] + pad[1] - (kh - 1) * dil[0] + 1
+    ow = w_ - 1 + pad[2] + pad[3] - (kw - 1) * dil[1] + 1
+    x = W._normal(r, (n, h, w_, cin), dtype)
+    wt = W._normal(r, (cout, kh, kw, cin), dtype)
+    g = GraphBuilder()
+    g.input("x", x.shape, dtype)
+    g.const("w", wt, dtype)
+    if out_dtype == "FP32":
+        bias = r.standard_normal(cout).astype(np.float32)
+        g.const("bias", bias, "FP32")
+        bias_f = bias.astype(np.float64)
+    else:
+        bias_bits = W._normal(r, (cout,), out_dtype)
+        g.const("bias", bias_bits, out_dtype)
+        bias_f = _f16_to_torch(bias_bits, out_dtype).numpy()
+    g.const("zx", np.array([0], np.uint16), dtype)
+    g.const("zw", np.array([0], np.uint16), dtype)
+    g.tensor("y", [n, oh, ow, cout], out_dtype)
+    g.op("CONV2D", ["x", "w", "bias", "zx", "zw"], ["y"], pad=list(pad), stride=[1, 1], dilation=list(dil),
+         acc_type="FP32")
+    got = run(g.build(["y"]), {"x": (x, dtype)})["y"].numpy()
+    if out_dtype != "FP32":
+        got = _f16_to_torch(got.view(np.uint16), out_dtype).numpy()
+    got = got.astype(np.float64)
+    tx = _f16_to_torch(x, dtype).permute(0, 3, 1, 2)
+    tw = _f16_to_torch(wt, dtype).permute(0, 3, 1, 2)
+    xp = torch.nn.functional.pad(tx, (pad[2], pad[3], pad[0], pad[1]))
+    acc = torch.nn.functional.conv2d(xp, tw, dilation=dil).permute(0, 2, 3, 1).numpy()
+    absy = torch.nn.functional.conv2d(xp.abs(), tw.abs(), dilation=dil).permute(0, 2, 3, 1).numpy()
+    exact = acc + bias_f
+    K = kh * kw * cin
+    u = {"FP32": 0.0, "BF16": 2.0 ** -8, "FP16": 2.0 ** -11}[out_dtype]
+    bound = 2 * K * 2.0 ** -24 * absy + 2.0 ** -24 * np.abs(exact) + 2 * u * (np.abs(acc) + np.abs(exact)) + 1e-30
+    assert np.all(np.abs(got - exact) <= bound), np.abs(got - exact).max()

@@ -179,6 +179,30 @@ struct GemmF16Desc {
 bool gemm_f16_supported(int64_t batch, int64_t m, int64_t n, int64_t k, bool b_kn, const void* a, const void* b);
 void gemm_f16(const GemmF16Desc& d, const void* a, const void* b, void* out, hipStream_t stream);
 
+// bf16 / fp16 CONV2D with fp32 accumulation on the stride-1 halo kernel
+// (the int8 headline kernel's float variant): NHWC x, OHWI w, f32 bias,
+// out = round(round(acc) + bias) in out_fmt (src/ops/conv.rs:475-496 with
+// AccF32). Applies to stride-1 convolutions with ic % 16 == 0, output rows
+// of at most 512 pixels and 16-byte aligned x and w:
+// conv_f16_halo_wpack_bytes(d) > 0 then, and conv_f16_halo runs with the
+// weights that conv_f16_halo_wpack packed into d.wpack.
+struct ConvF16Desc {
+    const void* x = nullptr;  // bf16 / fp16 [n, ih, iw, ic]
+    const void* w = nullptr;  // bf16 / fp16 [oc, kh, kw, ic]
+    GemmElem elem = ELEM_BF16;
+    int32_t n = 1, ih = 1, iw = 1, ic = 1, oc = 1, kh = 1, kw = 1, oh = 1, ow = 1;
+    int32_t pt = 0, pl = 0, sy = 1, sx = 1, dy = 1, dx = 1;
+    const float* bias = nullptr;  // [bias_len], bias_len 1 or oc
+    int32_t bias_len = 1;
+    FloatFmt out_fmt = FMT_F32;
+    const void* wpack = nullptr;
+};
+int64_t conv_f16_halo_wpack_bytes(const ConvF16Desc& d);
+// Output channels per block of that packing (0 when the kernel does not apply).
+int conv_f16_halo_block(const ConvF16Desc& d);
+void conv_f16_halo_wpack(const ConvF16Desc& d, void* wp, hipStream_t stream);
+void conv_f16_halo(const ConvF16Desc& d, void* out, hipStream_t stream);
+
 // ---------------------------------------------------------------------------
 // Reference-order kernels (one thread per output, the reference's loop
 // order and rounding, so float results are bit-identical to a sequential

@@ -28,6 +28,7 @@
 // the epilogue stores as one vector.
 #include <algorithm>
 
+#include <stdexcept>
 #include <type_traits>
 #include <vector>
 
@@ -763,6 +764,16 @@ __global__ void __launch_bounds__(HALO_NT, 2) conv_i8_halo_kernel(HaloArgs A)
 // stored after the table.
 // ---------------------------------------------------------------------------
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+// Element type of the halo kernel's operands: int8 (the table-driven
+// epilogue), or bf16 / fp16 with fp32 accumulation (the float epilogue
+// round(round(acc) + bias) of src/ops/conv.rs:493-495). The kernel works on
+// bytes: a float pass covers 16 channels (32 bytes), as an int8 pass covers
+// 32.
+enum HaloElem : int { HE_I8 = 0, HE_BF16 = 1, HE_F16 = 2 };
 
 struct Halo32Args {
     const int8_t* x;
@@ -774,7 +785,10 @@ struct Halo32Args {
     int32_t sbytes;  // LDS bytes of one halo stage (HR*HW*64, 1 KB multiple)
     int32_t wbytes;  // bytes of one pass's weights (taps * BC * 32)
     FastDiv div_ow, div_hw;
-    EpiArgs E;
+    EpiArgs E;          // int8: the table epilogue; float: out, N
+    const int8_t* zfill;  // 16 bytes loaded for padding taps: the input zero point (int8), zeros (float)
+    const float* fbias;   // float: per-channel bias as f32 values (or null)
+    int32_t fbias_len, fmt;
 };
 
 // Pixel slots of a workgroup with PG waves along the pixels, TB 32-pixel
@@ -797,6 +811,75 @@ __device__ __forceinline__ void dma16(const void* g, const void* l)
 
 // Weight row of MFMA row r (see above).
 __device__ __forceinline__ int h32_row_channel(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
+
+// One 32x32 MFMA step of the halo kernel: 16 bytes of A and B per lane (32
+// int8 or 16 bf16 / fp16 reduction elements).
+template <int EL, typename Acc>
+__device__ __forceinline__ Acc h32_mfma(const v4i& a, const v4i& b, const Acc& c)
+{
+    if constexpr (EL == HE_I8)
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+    else if constexpr (EL == HE_BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                       0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0,
+                                                      0);
+}
+
+// Float epilogue of the 32x32 layout (lane (h, l32) holds channels
+// 32 a + 16 h + 0..15 of tile pixel 32 (pw + PG b) + l32):
+// out = round(round(acc) + bias) in the output format, or acc for fp32
+// output without bias (src/ops/conv.rs:493-495). OB: output bytes (4 fp32,
+// 2 bf16 / fp16).
+template <int TA, int TB, int PG, int OB, typename PixelMap>
+__device__ __forceinline__ void epilogue32f(v16f (&acc)[TA][TB], int n0, int pw, int lane, const Halo32Args& A,
+                                            PixelMap pixel)
+{
+    const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int b = 0; b < TB; b++) {
+        const int64_t m = pixel(32 * (pw + PG * b) + l32);
+        if (m < 0)
+            continue;
+#pragma unroll
+        for (int a = 0; a < TA; a++) {
+            const int c0 = n0 + 32 * a + 16 * h;
+            if (c0 >= A.E.N)
+                continue;
+            uint32_t res[4 * OB];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int c = c0 + i < A.E.N ? c0 + i : A.E.N - 1;
+                float r = acc[a][b][i];
+                if (A.fbias)  // the file builds with -ffp-contract=off: no fused bias add
+                    r = round_fmt16(round_fmt16(r, A.fmt) + A.fbias[A.fbias_len == 1 ? 0 : c], A.fmt);
+                if constexpr (OB == 4) {
+                    res[i] = __builtin_bit_cast(uint32_t, r);
+                } else {
+                    const uint32_t bits = A.fmt == FMT_F16 ? f32_to_f16_bits(r) : f32_to_bf16_bits(r);
+                    res[i / 2] = (i & 1) ? (res[i / 2] | (bits << 16)) : bits;
+                }
+            }
+            uint8_t* dst = A.E.out + (m * A.E.N + c0) * OB;
+            if (c0 + 16 <= A.E.N && ((m * A.E.N + c0) * OB) % 16 == 0) {
+#pragma unroll
+                for (int wd = 0; wd < 4 * OB; wd += 4)
+                    *reinterpret_cast<v4u*>(dst + 4 * wd) = v4u{res[wd], res[wd + 1], res[wd + 2], res[wd + 3]};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    if (c0 + e >= A.E.N)
+                        continue;
+                    if constexpr (OB == 4)
+                        reinterpret_cast<uint32_t*>(dst)[e] = res[e];
+                    else
+                        reinterpret_cast<uint16_t*>(dst)[e] = uint16_t(res[e / 2] >> (16 * (e & 1)));
+                }
+            }
+        }
+    }
+}
 
 // Epilogue of the 32x32 layout: lane (h, l32) holds channels 32 a + 16 h +
 // 0..15 (counted from n0; s_tab starts at channel n0) of tile pixel
@@ -941,10 +1024,13 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
 // KT: taps when fixed at compile time (9 = 3x3; the tap loop is then fully
 // unrolled so that each tap waits only for its own fragments), 0 = any.
 // PG: waves along the pixels (each wave takes 64 channels), so BC / 64 * PG
-// waves in all; TB: 32-pixel tiles per wave.
-template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW>
+// waves in all; TB: 32-pixel tiles per wave; EL: HaloElem (the float kinds
+// have no zero points, RESCALE or table).
+template <int EL, int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW>
 __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Halo32Args A)
 {
+    static_assert(EL == HE_I8 || (!RS && !ZW), "float halo convolutions have no RESCALE or zero points");
+    using Acc = std::conditional_t<EL == HE_I8, v16i, v16f>;
     constexpr int NT = BC / 64 * PG * 64;  // threads
     constexpr int TA = 2;                  // 32-channel tiles per wave
     constexpr int BP = h32_bp(PG, TB);
@@ -977,7 +1063,7 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     const int passes = A.IC >> 5;
 
     // Epilogue table straight into LDS (channels past N repeat channel N-1).
-    if (tid < 2 * BC) {
+    if (EL == HE_I8 && tid < 2 * BC) {
         const int c = n0 + (tid >> 1);
         dma16(A.tab + 2 * (c < A.N ? c : A.N - 1) + (tid & 1), s_tab + wave * 64);
     }
@@ -987,9 +1073,13 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 
     // Additive constants of this lane's channels (cw + 32 a + 16 h + i for
     // result element i), fetched now and moved into the accumulators once
-    // the first loads have landed.
-    v16i acc[TA][TB], init[TA];
-    {
+    // the first loads have landed (int8; float accumulators start at 0).
+    Acc acc[TA][TB], init[TA];
+    if constexpr (EL != HE_I8) {
+#pragma unroll
+        for (int a = 0; a < TA; a++)
+            init[a] = Acc{};
+    } else {
         const int32_t* adds = reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1);
 #pragma unroll
         for (int a = 0; a < TA; a++) {
@@ -1027,7 +1117,7 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     }
 
     const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.IC;
-    const int8_t* const zfill = reinterpret_cast<const int8_t*>(A.tab + 2 * A.N);
+    const int8_t* const zfill = A.zfill;
     const int8_t* const wsrc = A.wp + int64_t(blockIdx.y) * passes * A.wbytes + lane * 16;
     const int nwq = taps * (BC / 32);  // 1 KB groups of one pass's weights
     auto dma_w = [&](int pass) {
@@ -1115,7 +1205,7 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
             for (int b = 0; b < TB; b++)
 #pragma unroll
                 for (int a = 0; a < TA; a++)
-                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a], fb[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = h32_mfma<EL>(fa[a], fb[b], acc[a][b]);
         };
         if (!live) {
             // no pixels: only the loads and barriers of the pass
@@ -1181,9 +1271,13 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     }
 
     const int m0 = (img * A.OH + oy0) * A.OW;
-    if (live)
-        epilogue32<TA, TB, PG, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
-                                       [&](int p) { return p < npix ? m0 + p : -1; });
+    if (live) {
+        if constexpr (EL == HE_I8)
+            epilogue32<TA, TB, PG, OB, RS, ZW>(acc, s_tab + 2 * cw, s_rowsum, n0 + cw, pw, lane, A.E,
+                                               [&](int p) { return p < npix ? m0 + p : -1; });
+        else
+            epilogue32f<TA, TB, PG, OB>(acc, n0 + cw, pw, lane, A, [&](int p) { return p < npix ? m0 + p : -1; });
+    }
 }
 
 // Packed weights of the 32x32 halo kernel: 16-byte slot
@@ -1807,10 +1901,10 @@ bool halo_plan(const ConvI8Desc& d, bool zw, HaloArgs& a, int& bc, int& kc, size
     return true;
 }
 
-template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW>
+template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW, int EL = HE_I8>
 void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t s)
 {
-    auto kfn = conv_i8_halo32_kernel<BC, PG, TB, KT, OB, RS, ZW>;
+    auto kfn = conv_i8_halo32_kernel<EL, BC, PG, TB, KT, OB, RS, ZW>;
     static bool attr = [&]() {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       HALO_LDS_MAX),
@@ -2215,6 +2309,7 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     Halo32Args h32{};
     if (!pw && d.wpack && halo32_plan(d, zw, h32, bc, lds, blocks)) {
         h32.tab = static_cast<const v4i*>(tab);
+        h32.zfill = reinterpret_cast<const int8_t*>(h32.tab + 2 * d.oc);
         h32.E = e;
         const bool k3 = d.kh == 3 && d.kw == 3;
         if (bc == 128) {
@@ -2291,6 +2386,154 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     } else {
         launch_tile<64, false>(a, ob, rs != nullptr, zw, stream);
     }
+}
+
+namespace {
+
+// The byte view of a float convolution that the halo planner and weight
+// packing take: every channel is two bytes.
+ConvI8Desc f16_byte_desc(const ConvF16Desc& d)
+{
+    ConvI8Desc b;
+    b.x = static_cast<const int8_t*>(d.x);
+    b.w = static_cast<const int8_t*>(d.w);
+    b.n = d.n;
+    b.ih = d.ih;
+    b.iw = d.iw;
+    b.ic = 2 * d.ic;
+    b.oc = d.oc;
+    b.kh = d.kh;
+    b.kw = d.kw;
+    b.oh = d.oh;
+    b.ow = d.ow;
+    b.pt = d.pt;
+    b.pl = d.pl;
+    b.dy = d.dy;
+    b.dx = d.dx;
+    b.wpack = static_cast<const int8_t*>(d.wpack);
+    return b;
+}
+
+bool f16_halo_ok(const ConvF16Desc& d)
+{
+    const bool aligned = (reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w)) % 16 == 0;
+    return aligned && d.sy == 1 && d.sx == 1 && d.ic % 16 == 0 && (d.elem == ELEM_BF16 || d.elem == ELEM_F16) &&
+           (d.out_fmt == FMT_F32 || d.out_fmt == FMT_BF16 || d.out_fmt == FMT_F16) &&
+           int64_t(d.n) * d.ih * d.iw * d.ic * 2 < (int64_t(1) << 31) &&
+           int64_t(d.n) * d.oh * d.ow * d.oc * 4 < (int64_t(1) << 31);
+}
+
+// Zeros for the padding taps of float halo convolutions (the int8 kind
+// loads the input zero point from its table instead); one address per
+// device, as hipGetSymbolAddress reports it.
+__device__ __attribute__((aligned(16))) int32_t h32_float_zeros[4];
+
+const int8_t* float_zeros()
+{
+    static const int8_t* addr[64] = {nullptr};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64)
+        throw std::runtime_error("conv_f16_halo: device index out of range");
+    if (!addr[dev]) {
+        void* p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(h32_float_zeros)), "halo zero fill");
+        addr[dev] = static_cast<const int8_t*>(p);
+    }
+    return addr[dev];
+}
+
+template <int BC, int PG, int TB, int KT, int EL>
+void launch_halo32_float(const Halo32Args& a, unsigned blocks, size_t lds, FloatFmt fmt, hipStream_t s)
+{
+    if (fmt == FMT_F32)
+        launch_halo32<BC, PG, TB, KT, 4, false, false, EL>(a, blocks, lds, s);
+    else
+        launch_halo32<BC, PG, TB, KT, 2, false, false, EL>(a, blocks, lds, s);
+}
+
+template <int EL>
+void launch_halo32_float_layout(const Halo32Args& a, int bc, unsigned blocks, size_t lds, bool k3, FloatFmt fmt,
+                                hipStream_t s)
+{
+    if (bc == 128) {
+        if (k3)
+            launch_halo32_float<128, 4, 2, 9, EL>(a, blocks, lds, fmt, s);
+        else
+            launch_halo32_float<128, 4, 2, 0, EL>(a, blocks, lds, fmt, s);
+    } else if (a.TB == 2) {
+        if (k3)
+            launch_halo32_float<64, 8, 2, 9, EL>(a, blocks, lds, fmt, s);
+        else
+            launch_halo32_float<64, 8, 2, 0, EL>(a, blocks, lds, fmt, s);
+    } else {
+        if (k3)
+            launch_halo32_float<64, 8, 1, 9, EL>(a, blocks, lds, fmt, s);
+        else
+            launch_halo32_float<64, 8, 1, 0, EL>(a, blocks, lds, fmt, s);
+    }
+}
+
+}  // namespace
+
+int conv_f16_halo_block(const ConvF16Desc& d)
+{
+    if (!f16_halo_ok(d))
+        return 0;
+    const ConvI8Desc b = f16_byte_desc(d);
+    Halo32Args a{};
+    int bc = 0;
+    size_t lds = 0;
+    unsigned blocks = 0;
+    return halo32_plan(b, false, a, bc, lds, blocks) ? bc : 0;
+}
+
+int64_t conv_f16_halo_wpack_bytes(const ConvF16Desc& d)
+{
+    const int bc = conv_f16_halo_block(d);
+    if (bc == 0)
+        return 0;
+    return int64_t((d.oc + bc - 1) / bc) * bc * d.kh * d.kw * 2 * d.ic;
+}
+
+void conv_f16_halo_wpack(const ConvF16Desc& d, void* wp, hipStream_t stream)
+{
+    const ConvI8Desc b = f16_byte_desc(d);
+    Halo32Args a{};
+    int bc = 0;
+    size_t lds = 0;
+    unsigned blocks = 0;
+    if (!f16_halo_ok(d) || !halo32_plan(b, false, a, bc, lds, blocks))
+        throw std::runtime_error("conv_f16_halo_wpack: the halo kernel does not apply");
+    const int64_t slots = int64_t((d.oc + bc - 1) / bc) * bc * d.kh * d.kw * b.ic / 16;
+    hipLaunchKernelGGL(conv_i8_wpack_kernel, dim3(unsigned((slots + 255) / 256)), dim3(256), 0, stream, b.w, d.oc,
+                       d.kh * d.kw * b.ic, b.ic, d.kh * d.kw, bc, slots, static_cast<v4u*>(wp));
+}
+
+void conv_f16_halo(const ConvF16Desc& d, void* out, hipStream_t stream)
+{
+    const ConvI8Desc b = f16_byte_desc(d);
+    Halo32Args a{};
+    int bc = 0;
+    size_t lds = 0;
+    unsigned blocks = 0;
+    if (!f16_halo_ok(d) || !d.wpack || !halo32_plan(b, false, a, bc, lds, blocks))
+        throw std::runtime_error("conv_f16_halo: the halo kernel does not apply");
+    if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)
+        return;
+    a.tab = nullptr;
+    a.zfill = float_zeros();
+    a.E = EpiArgs{};
+    a.E.out = static_cast<uint8_t*>(out);
+    a.E.N = d.oc;
+    a.fbias = d.bias;
+    a.fbias_len = d.bias_len;
+    a.fmt = d.out_fmt;
+    const bool k3 = d.kh == 3 && d.kw == 3;
+    if (d.elem == ELEM_BF16)
+        launch_halo32_float_layout<HE_BF16>(a, bc, blocks, lds, k3, d.out_fmt, stream);
+    else
+        launch_halo32_float_layout<HE_F16>(a, bc, blocks, lds, k3, d.out_fmt, stream);
 }
 
 }  // namespace kern

@@ -1026,7 +1026,42 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             fd.out_fmt = gd.out_fmt;
             kern::gemm_f16(fd, xd, wd, od, st.s());
         } else if (count > 0) {
-            kern::gemm(gd, xd, wd, od, st.err(), st.s());
+            kern::ConvF16Desc hd;
+            hd.x = xd;
+            hd.w = wd;
+            hd.elem = gd.elem;
+            hd.n = gd.n;
+            hd.ih = gd.ih;
+            hd.iw = gd.iw;
+            hd.ic = gd.ic;
+            hd.oc = gd.oc;
+            hd.kh = gd.kh;
+            hd.kw = gd.kw;
+            hd.oh = gd.oh;
+            hd.ow = gd.ow;
+            hd.pt = gd.pt;
+            hd.pl = gd.pl;
+            hd.sy = gd.sy;
+            hd.sx = gd.sx;
+            hd.dy = gd.dy;
+            hd.dx = gd.dx;
+            hd.bias = static_cast<const float*>(gd.bias);
+            hd.bias_len = gd.bias_len;
+            hd.out_fmt = gd.out_fmt;
+            const int64_t wpb = kern::conv_f16_halo_wpack_bytes(hd);
+            if (wpb > 0) {
+                // Stride-1 convolution on the halo kernel, with its packed
+                // weights cached on a constant weight.
+                const bool w_const = st.const_defs.count(op.inputs[1]) != 0;
+                const std::string key =
+                    "conv_f16_wpack:" + std::to_string(wpb) + ":" + std::to_string(kern::conv_f16_halo_block(hd));
+                auto wp = derived_i8(*weight->data, key, wpb, w_const, st.s(),
+                                     [&](void* dst) { kern::conv_f16_halo_wpack(hd, dst, st.s()); });
+                hd.wpack = wp->device_in();
+                kern::conv_f16_halo(hd, od, st.s());
+            } else {
+                kern::gemm(gd, xd, wd, od, st.err(), st.s());
+            }
         }
         st.set(out);
         return;
