@@ -1783,13 +1783,36 @@ void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
 
 // Channel tile with the least padded channel work (the 128-channel tile
 // skips a 64-channel half past N), the wider tile on a tie: the epilogue's
-// per-output work dominates layers with few reduction steps.
+// per-output work dominates layers with few reduction steps. Pointwise
+// layers weigh the input's re-reads per channel block instead.
 template <int KC, bool PW>
 void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
 {
     const int64_t n = a.N;
     const int64_t w128 = (n + 63) / 64 * 64, w64 = (n + 63) / 64 * 64, w32 = (n + 31) / 32 * 32,
                   w16 = (n + 15) / 16 * 16;
+    if (PW && a.M >= 32768) {
+        // Pointwise layers over many pixels are mostly memory-bound (a 1x1
+        // convolution reads K bytes per pixel and channel block): cost =
+        // re-reads of the input per channel block, weighted 64 to 1 against
+        // the padded channel work. The widest tile wins ties. (Over few
+        // pixels, narrow tiles give the workgroups that fill the chip.)
+        const int64_t cost[4] = {64 * ((n + 127) / 128) + w128, 64 * ((n + 63) / 64) + (n + 63) / 64 * 64,
+                                 64 * ((n + 31) / 32) + w32, 64 * ((n + 15) / 16) + w16};
+        int best = 0;
+        for (int i = 1; i < 4; i++)
+            if (cost[i] < cost[best])
+                best = i;
+        if (best == 0)
+            launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s);
+        else if (best == 1)
+            launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+        else if (best == 2)
+            launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+        else
+            launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+        return;
+    }
     if (w128 <= w32 && w128 <= w16 && n > 64)
         launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s);
     else if (w64 <= w32 && w64 <= w16 && n > 32)
