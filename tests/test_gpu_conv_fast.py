@@ -535,3 +535,44 @@ def test_range_bound_runtime_bias(case):
     check stays on, values inside the range pass."""
     graph, out, ins = _range_edge(case, over=False, bias_input=True)
     check(graph, out, ins)
+
+
+# 1x1 convolutions with K <= 64, N a multiple of 32, at least 4096 pixels
+# and an int8 RESCALE take the streaming pointwise kernel: every
+# channel-tile count (TA 1-4, and N past 128 in several blocks), one and two
+# reduction steps (K = 16 and 48 leave a zero-filled half step), nonzero
+# weight zero points, shifts below 32 (range check live), a fused CLAMP and
+# pixel counts that are not a multiple of 32; the last case (N = 24) stays
+# on the tiled kernel.
+PWS = [
+    # n, h, w, ic, oc
+    (1, 64, 64, 16, 96),
+    (2, 48, 47, 32, 32),
+    (1, 65, 67, 48, 64),
+    (3, 40, 40, 64, 192),
+    (1, 70, 64, 32, 384),
+    (2, 50, 41, 16, 128),
+    (1, 80, 80, 64, 160),
+    (2, 48, 47, 32, 24),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PWS)))
+def test_pointwise_stream(case):
+    n, h, w_, ic, oc = PWS[case]
+    rng = np.random.default_rng(9300 + case)
+    x = rng.integers(-128, 128, size=(n, h, w_, ic)).astype(np.int8)
+    zx = int(rng.integers(-128, 128))
+    zw = int(rng.integers(-5, 6)) if case % 2 else 0
+    if case % 3 == 2:
+        w = rng.integers(-2, 3, size=(oc, 1, 1, ic)).astype(np.int8)
+        bias = rng.integers(-1000, 1000, size=oc).astype(np.int32)
+        shift = rng.integers(24, 32, size=oc)
+    else:
+        w = rng.integers(-128, 128, size=(oc, 1, 1, ic)).astype(np.int8)
+        bias = rng.integers(-2 ** 31, 2 ** 31, size=oc).astype(np.int32)
+        shift = rng.integers(36, 50, size=oc)
+    rs = (rng.integers(2 ** 30, 2 ** 31, size=oc), shift, int(rng.integers(-16, 17)), bool(case % 2), True)
+    clamp = (int(rng.integers(-128, 0)), 100) if case % 3 == 0 else None
+    graph, out = build(x, w, bias, zx, zw, [0, 0, 0, 0], [1, 1], [1, 1], rescale=rs, clamp=clamp)
+    check(graph, out, {"x": (x, "INT8")})

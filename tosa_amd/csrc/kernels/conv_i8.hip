@@ -1280,6 +1280,121 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming pointwise int8 convolution for short reductions (1x1, stride 1,
+// K <= 64): a layer that moves K bytes in and N bytes out per pixel is
+// memory-bound, and the tiled kernels' per-workgroup staging and barriers
+// cost more than its MFMAs. Here the weights of a 32 TA-channel block live
+// in VGPRs (A fragments in the halo kernel's row order, loaded once), the
+// table in LDS, and every wave walks 32-pixel tiles on its own (no barriers
+// after the prologue): per tile KS 16-byte loads per lane straight into B
+// fragments (the next tile's are in flight while this one computes), TA x
+// KS v_mfma_i32_32x32x32_i8, and the 32x32 epilogue. Reduction bytes past K
+// load as zeros on both sides, so they add nothing to the dot products or to
+// the weight zero point's per-pixel sums; the table's terms use the real K.
+// ---------------------------------------------------------------------------
+struct PwsArgs {
+    const int8_t* x;  // [M][K]
+    const int8_t* w;  // [N][K]
+    const v4i* tab;
+    int32_t M, K, N;
+    int32_t ntiles;  // 32-pixel tiles
+    EpiArgs E;
+};
+
+template <int TA, int KS, int OB, bool RS, bool ZW>
+__global__ void __launch_bounds__(256, 2) conv_i8_pws_kernel(PwsArgs A)
+{
+    __shared__ v4i s_tab[2 * 32 * TA];
+    __shared__ __attribute__((aligned(16))) int32_t s_add[32 * TA];  // additive constants
+    __shared__ int32_t s_rowsum[4][32];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.y * 32 * TA;
+
+    // Table entries of the block's channels (past N: channel N - 1).
+    for (int i = tid; i < 2 * 32 * TA; i += 256) {
+        const int c = n0 + (i >> 1);
+        s_tab[i] = A.tab[2 * (c < A.N ? c : A.N - 1) + (i & 1)];
+    }
+    const int32_t* adds = reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1);
+    for (int i = tid; i < 32 * TA; i += 256)
+        s_add[i] = adds[n0 + i < A.N ? n0 + i : A.N - 1];
+    // A fragments: lane (row r = l32, k-half h) of channel tile a, step j
+    // holds bytes 32 j + 16 h .. + 15 of channel n0 + 32 a + h32_row_channel(r).
+    v4i wa[TA][KS];
+#pragma unroll
+    for (int a = 0; a < TA; a++) {
+        const int c = n0 + 32 * a + h32_row_channel(l32);
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const int k = 32 * j + 16 * h;
+            wa[a][j] = (c < A.N && k < A.K) ? *reinterpret_cast<const v4i*>(A.w + int64_t(c) * A.K + k) : v4i{0, 0, 0, 0};
+        }
+    }
+    __syncthreads();
+
+    const int step = gridDim.x * 4;
+    int t = blockIdx.x * 4 + wave;
+    auto load_b = [&](int tile, v4i(&fb)[KS]) {
+        const int p = 32 * tile + l32;
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const int k = 32 * j + 16 * h;
+            fb[j] = (p < A.M && k < A.K) ? *reinterpret_cast<const v4i*>(A.x + int64_t(p) * A.K + k) : v4i{0, 0, 0, 0};
+        }
+    };
+    v4i fb[KS], fn[KS];
+    if (t < A.ntiles)
+        load_b(t, fb);
+    for (; t < A.ntiles; t += step) {
+        if (t + step < A.ntiles)
+            load_b(t + step, fn);
+        if constexpr (ZW) {
+            // Per-pixel sum of the input bytes: this lane's 16 bytes per
+            // step, plus the other k-half's (lane l32 + 32).
+            int32_t sx = 0;
+#pragma unroll
+            for (int j = 0; j < KS; j++) {
+                sx = __builtin_amdgcn_sdot4(fb[j].x, 0x01010101, sx, false);
+                sx = __builtin_amdgcn_sdot4(fb[j].y, 0x01010101, sx, false);
+                sx = __builtin_amdgcn_sdot4(fb[j].z, 0x01010101, sx, false);
+                sx = __builtin_amdgcn_sdot4(fb[j].w, 0x01010101, sx, false);
+            }
+            sx += __shfl_xor(sx, 32);
+            if (h == 0)
+                s_rowsum[wave][l32] = sx;
+            __builtin_amdgcn_wave_barrier();
+        }
+        v16i acc[TA][1];
+#pragma unroll
+        for (int a = 0; a < TA; a++) {
+            // Additive constants of this lane's result channels 32 a + 16 h + i.
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const v4i v = *reinterpret_cast<const v4i*>(s_add + 32 * a + 16 * h + 4 * q);
+                acc[a][0][4 * q] = v.x;
+                acc[a][0][4 * q + 1] = v.y;
+                acc[a][0][4 * q + 2] = v.z;
+                acc[a][0][4 * q + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < KS; j++)
+                acc[a][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[a][j], fb[j], acc[a][0], 0, 0, 0);
+        }
+        const int p0 = 32 * t;
+        epilogue32<TA, 1, 1, OB, RS, ZW>(acc, s_tab, s_rowsum[wave], n0, 0, lane, A.E,
+                                         [&](int p) { return p0 + p < A.M ? int64_t(p0 + p) : int64_t(-1); });
+        if constexpr (ZW)
+            __builtin_amdgcn_wave_barrier();  // the row sums are read before the next tile's
+#pragma unroll
+        for (int j = 0; j < KS; j++)
+            fb[j] = fn[j];
+    }
+}
+
 // Packed weights of the 32x32 halo kernel: 16-byte slot
 // ((((nb passes + p) taps + t) TA + a) 64 + l) holds bytes 32 p + 16 (l / 32)
 // .. + 15 of tap t of channel nb BC + 32 a + row_channel(l % 32) (zero past
@@ -1737,6 +1852,43 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
     reinterpret_cast<int32_t*>(tab + 2 * N + 1)[c] = int32_t(add);
     tab[2 * c + 1] = v4i{int32_t(uint32_t(uint64_t(rp))), int32_t(uint64_t(rp) >> 32),
                          int32_t(uint32_t(uint64_t(rn))), int32_t(uint64_t(rn) >> 32)};
+}
+
+int cu_count();
+
+template <int TA, int KS, bool ZW>
+void launch_pws(const PwsArgs& a, hipStream_t s)
+{
+    const unsigned wgs = unsigned(std::min<int64_t>((a.ntiles + 3) / 4, int64_t(2) * cu_count()));
+    hipLaunchKernelGGL((conv_i8_pws_kernel<TA, KS, 1, true, ZW>), dim3(wgs, unsigned((a.N + 32 * TA - 1) / (32 * TA))),
+                       dim3(256), 0, s, a);
+}
+
+// Channel tiles per block: the most of 4, 3, 2, 1 that divide N / 32.
+template <int KS, bool ZW>
+void launch_pws_ta(const PwsArgs& a, hipStream_t s)
+{
+    const int t = a.N / 32;
+    if (t % 4 == 0)
+        launch_pws<4, KS, ZW>(a, s);
+    else if (t % 3 == 0)
+        launch_pws<3, KS, ZW>(a, s);
+    else if (t % 2 == 0)
+        launch_pws<2, KS, ZW>(a, s);
+    else
+        launch_pws<1, KS, ZW>(a, s);
+}
+
+// The streaming pointwise kernel takes 1x1 stride-1 convolutions with
+// K = ic a multiple of 16 up to 64, N a multiple of 32 (its epilogue works on
+// whole 32-channel tiles: with N = 16, 24 or 144 the padded channels made it
+// no faster than the tiled kernel), many pixels (its persistent waves need
+// tiles to walk) and the fused RESCALE to int8.
+bool pws_applies(const ConvI8Desc& d, bool pw, int ob, const RescaleDev* rs)
+{
+    const int64_t m = int64_t(d.n) * d.oh * d.ow;
+    return pw && d.batch == 1 && rs && ob == 1 && d.ic % 16 == 0 && d.ic <= 64 && d.oc % 32 == 0 && m >= 4096 &&
+           m * d.ic < (int64_t(1) << 31) && (reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w)) % 16 == 0;
 }
 
 template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW>
@@ -2325,6 +2477,29 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     }
     const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
                     d.iw == d.ow;
+    if (pws_applies(d, pw, ob, rs)) {
+        PwsArgs a{};
+        a.x = d.x;
+        a.w = d.w;
+        a.tab = static_cast<const v4i*>(tab);
+        a.M = d.n * d.oh * d.ow;
+        a.K = d.ic;
+        a.N = d.oc;
+        a.ntiles = (a.M + 31) / 32;
+        a.E = e;
+        if (d.ic <= 32) {
+            if (zw)
+                launch_pws_ta<1, true>(a, stream);
+            else
+                launch_pws_ta<1, false>(a, stream);
+        } else {
+            if (zw)
+                launch_pws_ta<2, true>(a, stream);
+            else
+                launch_pws_ta<2, false>(a, stream);
+        }
+        return;
+    }
 
     int bc = 128, kc = 128;
     size_t lds = 0;
