@@ -781,7 +781,7 @@ struct Halo32Args {
     const v4i* tab;    // [N][2] entries, 16 bytes of the input zero point, [N] additive constants
     int32_t N, IC, IH, IW, OH, OW, KW, taps, dy, dx, pt, pl;
     int32_t R, tiles_per_img, HR, HW;
-    int32_t PG, TB;  // waves along the pixels, 32-pixel tiles per wave: the launch's template
+    int32_t PG, TB, KP;  // waves along the pixels, 32-pixel tiles per wave, units per pass: the launch's template
     int32_t sbytes;  // LDS bytes of one halo stage (HR*HW*64, 1 KB multiple)
     int32_t wbytes;  // bytes of one pass's weights (taps * BC * 32)
     FastDiv div_ow, div_hw;
@@ -1025,10 +1025,13 @@ __device__ __forceinline__ void epilogue32(v16i (&acc)[TA][TB], const v4i* s_tab
 // unrolled so that each tap waits only for its own fragments), 0 = any.
 // PG: waves along the pixels (each wave takes 64 channels), so BC / 64 * PG
 // waves in all; TB: 32-pixel tiles per wave; EL: HaloElem (the float kinds
-// have no zero points, RESCALE or table).
-template <int EL, int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW>
+// have no zero points, RESCALE or table); KP: 32-byte reduction units per
+// pass (2: each pass covers a whole 64-byte halo stage, half the barriers and
+// load bursts of KP 1, twice the weight buffer).
+template <int EL, int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW, int KP = 1>
 __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Halo32Args A)
 {
+    static_assert(KP == 1 || KP == 2, "one or two reduction units per pass");
     static_assert(EL == HE_I8 || (!RS && !ZW), "float halo convolutions have no RESCALE or zero points");
     using Acc = std::conditional_t<EL == HE_I8, v16i, v16f>;
     constexpr int NT = BC / 64 * PG * 64;  // threads
@@ -1038,7 +1041,7 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* const halo = smem;                                          // [2][sbytes]
     uint8_t* const wbuf = smem + 2 * A.sbytes;                           // [2][wbytes]
-    v4i* const s_tab = reinterpret_cast<v4i*>(wbuf + 2 * A.wbytes);     // [2 BC]
+    v4i* const s_tab = reinterpret_cast<v4i*>(wbuf + 2 * KP * A.wbytes);  // [2 BC]
     int32_t* const s_hsum = reinterpret_cast<int32_t*>(s_tab + 2 * BC);  // ZW: [HR HW]
     int32_t* const s_rowsum = s_hsum + A.HR * A.HW;                      // ZW: [BP]
 
@@ -1060,7 +1063,8 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     const int n0 = blockIdx.y * BC;
     const int hw = A.HR * A.HW;
     const int taps = KT > 0 ? KT : A.taps;
-    const int passes = A.IC >> 5;
+    const int passes = A.IC >> 5;  // 32-byte reduction units; the loop takes KP per pass
+    const int npass = passes / KP;
 
     // Epilogue table straight into LDS (channels past N repeat channel N-1).
     if (EL == HE_I8 && tid < 2 * BC) {
@@ -1121,9 +1125,9 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
     const int8_t* const wsrc = A.wp + int64_t(blockIdx.y) * passes * A.wbytes + lane * 16;
     const int nwq = taps * (BC / 32);  // 1 KB groups of one pass's weights
     auto dma_w = [&](int pass) {
-        const int8_t* src = wsrc + int64_t(pass) * A.wbytes;
-        uint8_t* dst = wbuf + (pass & 1) * A.wbytes;
-        for (int j = wave; j < nwq; j += NT / 64)
+        const int8_t* src = wsrc + int64_t(pass) * KP * A.wbytes;
+        uint8_t* dst = wbuf + (pass & 1) * KP * A.wbytes;
+        for (int j = wave; j < KP * nwq; j += NT / 64)
             dma16(src + j * 1024, dst + j * 1024);
     };
     // Halo stage st (input channels 64 st ..): 16-byte slot s of the LDS
@@ -1148,7 +1152,7 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 
     dma_halo(0);
     dma_w(0);
-    for (int pass = 0; pass < passes; pass++) {
+    for (int pass = 0; pass < npass; pass++) {
         // The loads of this pass (issued one pass earlier, or above) have
         // landed, and every wave is done with the buffers the next loads
         // overwrite.
@@ -1161,13 +1165,16 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
                 for (int b = 0; b < TB; b++)
                     acc[a][b] = init[a];
         }
-        const int st = pass >> 1;
-        if ((pass & 1) == 0 && 2 * (st + 1) < passes)
+        // Halo stage of this pass; a pass that opens a stage also loads
+        // the next one.
+        const int st = KP == 2 ? pass : pass >> 1;
+        const bool opens = KP == 2 || (pass & 1) == 0;
+        if (opens && 2 * (st + 1) < passes)
             dma_halo(st + 1);
-        if (pass + 1 < passes)
+        if (pass + 1 < npass)
             dma_w(pass + 1);
         if constexpr (ZW) {
-            if ((pass & 1) == 0) {
+            if (opens) {
                 const uint8_t* hs = halo + (st & 1) * A.sbytes;
                 for (int hp = tid; hp < hw; hp += NT) {
                     int32_t t = s_hsum[hp];
@@ -1185,32 +1192,39 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
                 }
             }
         }
-        const uint8_t* const wb = wbuf + (pass & 1) * A.wbytes + lane * 16;
+        const uint8_t* const wb = wbuf + (pass & 1) * KP * A.wbytes + lane * 16;
         const uint8_t* const hb = halo + (st & 1) * A.sbytes;
-        const int cl = 2 * (pass & 1) + h;  // logical chunk of this lane's k-half
-        // The fragments of tap t + 1 are read while tap t's MFMAs run.
-        auto load = [&](v4i(&fa)[TA], v4i(&fb)[TB], int t, int ky, int kx) {
-#pragma unroll
-            for (int a = 0; a < TA; a++)
-                fa[a] = *reinterpret_cast<const v4i*>(wb + (t * (BC / 32) + cw / 32 + a) * 1024);
+        // The fragments of tap t + 1 are read while tap t's MFMAs run. Unit
+        // u of the pass: weights at u wbytes in the pass's buffer, halo
+        // logical chunk 2 u + h (KP 2) or 2 (pass & 1) + h (KP 1).
+        auto load = [&](v4i(&fa)[KP][TA], v4i(&fb)[KP][TB], int t, int ky, int kx) {
             const int off = ky * A.dy * A.HW + kx * A.dx;
 #pragma unroll
-            for (int b = 0; b < TB; b++) {
-                const int hp = hpos[b] + off;
-                fb[b] = *reinterpret_cast<const v4i*>(hb + (hp * 4 + (cl ^ ((hp >> 2) & 3))) * 16);
-            }
-        };
-        auto mfma = [&](const v4i(&fa)[TA], const v4i(&fb)[TB]) {
-#pragma unroll
-            for (int b = 0; b < TB; b++)
+            for (int u = 0; u < KP; u++) {
 #pragma unroll
                 for (int a = 0; a < TA; a++)
-                    acc[a][b] = h32_mfma<EL>(fa[a], fb[b], acc[a][b]);
+                    fa[u][a] = *reinterpret_cast<const v4i*>(wb + u * A.wbytes + (t * (BC / 32) + cw / 32 + a) * 1024);
+                const int cl = KP == 2 ? 2 * u + h : 2 * (pass & 1) + h;
+#pragma unroll
+                for (int b = 0; b < TB; b++) {
+                    const int hp = hpos[b] + off;
+                    fb[u][b] = *reinterpret_cast<const v4i*>(hb + (hp * 4 + (cl ^ ((hp >> 2) & 3))) * 16);
+                }
+            }
+        };
+        auto mfma = [&](const v4i(&fa)[KP][TA], const v4i(&fb)[KP][TB]) {
+#pragma unroll
+            for (int u = 0; u < KP; u++)
+#pragma unroll
+                for (int b = 0; b < TB; b++)
+#pragma unroll
+                    for (int a = 0; a < TA; a++)
+                        acc[a][b] = h32_mfma<EL>(fa[u][a], fb[u][b], acc[a][b]);
         };
         if (!live) {
             // no pixels: only the loads and barriers of the pass
         } else if constexpr (KT == 9) {
-            v4i fa[2][TA], fb[2][TB];
+            v4i fa[2][KP][TA], fb[2][KP][TB];
             load(fa[0], fb[0], 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < 9; t++) {
@@ -1232,7 +1246,7 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
                     ky++;
                 }
             };
-            v4i fa0[TA], fb0[TB], fa1[TA], fb1[TB];
+            v4i fa0[KP][TA], fb0[KP][TB], fa1[KP][TA], fb1[KP][TB];
             load(fa0, fb0, 0, 0, 0);
             step();
             for (int t = 0; t < taps; t += 2) {
@@ -2076,10 +2090,10 @@ bool halo_plan(const ConvI8Desc& d, bool zw, HaloArgs& a, int& bc, int& kc, size
     return true;
 }
 
-template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW, int EL = HE_I8>
+template <int BC, int PG, int TB, int KT, int OB, bool RS, bool ZW, int EL = HE_I8, int KP = 1>
 void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t s)
 {
-    auto kfn = conv_i8_halo32_kernel<EL, BC, PG, TB, KT, OB, RS, ZW>;
+    auto kfn = conv_i8_halo32_kernel<EL, BC, PG, TB, KT, OB, RS, ZW, KP>;
     static bool attr = [&]() {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                       HALO_LDS_MAX),
@@ -2090,21 +2104,21 @@ void launch_halo32(const Halo32Args& a, unsigned blocks, size_t lds, hipStream_t
     hipLaunchKernelGGL(kfn, dim3(blocks, (a.N + BC - 1) / BC), dim3(BC / 64 * PG * 64), lds, s, a);
 }
 
-template <int BC, int PG, int TB, int KT>
+template <int BC, int PG, int TB, int KT, int KP = 1>
 void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob, bool rs, bool zw, hipStream_t s)
 {
     if (!rs) {
         if (zw)
-            launch_halo32<BC, PG, TB, KT, 4, false, true>(a, blocks, lds, s);
+            launch_halo32<BC, PG, TB, KT, 4, false, true, HE_I8, KP>(a, blocks, lds, s);
         else
-            launch_halo32<BC, PG, TB, KT, 4, false, false>(a, blocks, lds, s);
+            launch_halo32<BC, PG, TB, KT, 4, false, false, HE_I8, KP>(a, blocks, lds, s);
         return;
     }
-#define TOSA_HALO32_OB(OBV)                                               \
-    if (zw)                                                               \
-        launch_halo32<BC, PG, TB, KT, OBV, true, true>(a, blocks, lds, s); \
-    else                                                                  \
-        launch_halo32<BC, PG, TB, KT, OBV, true, false>(a, blocks, lds, s);
+#define TOSA_HALO32_OB(OBV)                                                          \
+    if (zw)                                                                          \
+        launch_halo32<BC, PG, TB, KT, OBV, true, true, HE_I8, KP>(a, blocks, lds, s); \
+    else                                                                             \
+        launch_halo32<BC, PG, TB, KT, OBV, true, false, HE_I8, KP>(a, blocks, lds, s);
     if (ob == 1) {
         TOSA_HALO32_OB(1)
     } else if (ob == 2) {
@@ -2143,15 +2157,16 @@ int cu_count()
 // CU) x (that sum + 2), the 2 standing for a tile's fixed cost (first
 // loads, epilogue); ties go to the fewest bytes loaded per CU (weights +
 // halo: the loads' issue holds up the waves that make them).
-bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& lds, unsigned& blocks)
+bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& lds, unsigned& blocks,
+                 bool allow_kp2 = true)
 {
     if (d.sy != 1 || d.sx != 1 || d.ic % 32 != 0 || d.ow > H32_BP_MAX || d.oh < 1 || d.ow < 1 || d.depthwise)
         return false;
     const int taps = d.kh * d.kw;
     const int HW = d.ow + (d.kw - 1) * d.dx;
-    auto lds_for = [&](int R, int c, int bp) {
+    auto lds_for = [&](int R, int c, int bp, int kp = 1) {
         const size_t hw = (size_t(R) + size_t(d.kh - 1) * d.dy) * HW;
-        size_t b = 2 * ((hw * 64 + 1023) / 1024 * 1024) + 2 * size_t(taps) * c * 32 + size_t(32) * c;
+        size_t b = 2 * ((hw * 64 + 1023) / 1024 * 1024) + 2 * size_t(kp) * taps * c * 32 + size_t(32) * c;
         if (zw)
             b += size_t(4) * (hw + bp);
         return b;
@@ -2218,9 +2233,16 @@ bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& l
     a.wbytes = taps * bc * 32;
     a.PG = PG;
     a.TB = TB;
+    // Whole 64-byte stages per pass where the kernel has that variant (the
+    // 64-channel two-tile layout, 3x3 taps) and the doubled weight buffer
+    // fits.
+    a.KP = allow_kp2 && bc == 64 && PG == 8 && TB == 2 && taps == 9 && d.ic % 64 == 0 &&
+                   lds_for(R, bc, h32_bp(PG, TB), 2) <= size_t(HALO_LDS_MAX)
+               ? 2
+               : 1;
     a.div_ow = FastDiv(uint32_t(d.ow));
     a.div_hw = FastDiv(uint32_t(HW));
-    lds = lds_for(R, bc, h32_bp(PG, TB));
+    lds = lds_for(R, bc, h32_bp(PG, TB), a.KP);
     blocks = unsigned(d.n) * unsigned(a.tiles_per_img);
     return true;
 }
@@ -2516,7 +2538,9 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
             else
                 launch_halo32_epi<128, 4, 2, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
         } else if (h32.TB == 2) {
-            if (k3)
+            if (k3 && h32.KP == 2)
+                launch_halo32_epi<64, 8, 2, 9, 2>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
+            else if (k3)
                 launch_halo32_epi<64, 8, 2, 9>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
             else
                 launch_halo32_epi<64, 8, 2, 0>(h32, blocks, lds, ob, rs != nullptr, zw, stream);
@@ -2683,7 +2707,7 @@ int conv_f16_halo_block(const ConvF16Desc& d)
     int bc = 0;
     size_t lds = 0;
     unsigned blocks = 0;
-    return halo32_plan(b, false, a, bc, lds, blocks) ? bc : 0;
+    return halo32_plan(b, false, a, bc, lds, blocks, false) ? bc : 0;
 }
 
 int64_t conv_f16_halo_wpack_bytes(const ConvF16Desc& d)
@@ -2701,7 +2725,7 @@ void conv_f16_halo_wpack(const ConvF16Desc& d, void* wp, hipStream_t stream)
     int bc = 0;
     size_t lds = 0;
     unsigned blocks = 0;
-    if (!f16_halo_ok(d) || !halo32_plan(b, false, a, bc, lds, blocks))
+    if (!f16_halo_ok(d) || !halo32_plan(b, false, a, bc, lds, blocks, false))
         throw std::runtime_error("conv_f16_halo_wpack: the halo kernel does not apply");
     const int64_t slots = int64_t((d.oc + bc - 1) / bc) * bc * d.kh * d.kw * b.ic / 16;
     hipLaunchKernelGGL(conv_i8_wpack_kernel, dim3(unsigned((slots + 255) / 256)), dim3(256), 0, stream, b.w, d.oc,
@@ -2715,7 +2739,7 @@ void conv_f16_halo(const ConvF16Desc& d, void* out, hipStream_t stream)
     int bc = 0;
     size_t lds = 0;
     unsigned blocks = 0;
-    if (!f16_halo_ok(d) || !d.wpack || !halo32_plan(b, false, a, bc, lds, blocks))
+    if (!f16_halo_ok(d) || !d.wpack || !halo32_plan(b, false, a, bc, lds, blocks, false))
         throw std::runtime_error("conv_f16_halo: the halo kernel does not apply");
     if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)
         return;
