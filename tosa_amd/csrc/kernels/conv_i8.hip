@@ -1654,8 +1654,6 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
     const int p0 = ptile * (16 * TN);
     if (p0 >= A.P)
         return;
-    const uint32_t zf = uint32_t(uint8_t(A.zp_x)) * 0x01010101u;
-    const v4u zfill = v4u{zf, zf, zf, zf};
 
     // Input offsets of this lane's pixel in each tile (without the tap) and
     // the tap of each of its k-chunks: tap 4 g + grp of group g.
@@ -1716,6 +1714,21 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
         for (int i = 0; i < 4; i++)
             hi[i] = ~t0[i].z;
         uint32_t bad_bits = 0;
+        // Every tap of the wave's four tiles is loaded before the first
+        // MFMA: padding taps read the table's 16 bytes of input zero point,
+        // so no load is conditional (a select after the load lets the
+        // compiler put each load behind a branch and wait for it alone).
+        const int8_t* const zfill = reinterpret_cast<const int8_t*>(A.tab + 2 * A.C);
+        v4u xin[TN][G];
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const int iy = iy0[tn] + tdy[g];
+                const int ix = ix0[tn] + tdx[g];
+                const bool ok = tok[g] && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
+                xin[tn][g] = ld16(ok ? A.x + (pbase[tn] + iy * A.IW + ix) * A.C + c0 : zfill);
+            }
         // RC: some shift is below 32, so the value-range REQUIRE is checked.
         auto tiles = [&](auto rc) {
             constexpr bool RC = decltype(rc)::value;
@@ -1724,11 +1737,7 @@ __global__ void __launch_bounds__(256, 4) conv_i8_dw_kernel(DwArgs A)
             v4i acc = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const int iy = iy0[tn] + tdy[g];
-                const int ix = ix0[tn] + tdx[g];
-                const bool ok = tok[g] && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
-                const v4u v = ld16(A.x + (ok ? (pbase[tn] + iy * A.IW + ix) * A.C + c0 : 0));
-                const v4i bx = __builtin_bit_cast(v4i, ok ? v : zfill);
+                const v4i bx = __builtin_bit_cast(v4i, xin[tn][g]);
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, acc, 0, 0, 0);
                 if constexpr (ZW)
                     acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc1, 0, 0, 0);
