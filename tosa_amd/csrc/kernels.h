@@ -149,11 +149,19 @@ void conv_i8_im2col(const ConvI8Desc& d, int8_t* xcol, hipStream_t stream);
 void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t* out, hipStream_t stream);
 // MATMUL right operand [batch][c][w] -> [batch][w][c] (c % 16 == 0).
 void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream);
+// Compute units of the current device.
+int cu_count();
 // DEPTHWISE_CONV2D (multiplier 1, ic % 16 == 0, at most 12 taps) over
 // LDS-staged input tiles (dw_i8.hip); false when the shape does not fit its
 // LDS budget. Same table and epilogue contract as conv_i8_fast.
 bool depthwise_i8_lds(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
                       hipStream_t stream);
+// The same over a persistent grid that loads each (image, rows, channel
+// chunk) tile into LDS by direct global -> LDS loads while the previous tile
+// computes (dw_i8.hip); false for shapes it does not take (16-byte aligned
+// input and weights, tiles within its LDS budget).
+bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                       hipStream_t stream);
 // The convolution; `rs` selects the fused RESCALE (+CLAMP) epilogue with the
 // table built for the same `rs`, else the int32 output (conv + bias).
 void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,

@@ -1877,8 +1877,6 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
                          int32_t(uint32_t(uint64_t(rn))), int32_t(uint64_t(rn) >> 32)};
 }
 
-int cu_count();
-
 template <int TA, int KS, bool ZW>
 void launch_pws(const PwsArgs& a, hipStream_t s)
 {
@@ -2138,6 +2136,8 @@ void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob,
 #undef TOSA_HALO32_OB
 }
 
+}  // namespace
+
 // Compute units of the current device (workgroups of the 32x32 halo kernel
 // that run at once: its LDS allows one per CU).
 int cu_count()
@@ -2154,6 +2154,8 @@ int cu_count()
     }
     return counts[dev];
 }
+
+namespace {
 
 // Geometry of the 32x32 halo kernel for `d`, or false when it does not
 // apply: stride 1, ic a multiple of 32, output rows of at most 512 pixels,
@@ -2472,7 +2474,7 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)
         return;
     const bool zw = d.zp_w != 0;
-    if (d.depthwise && depthwise_i8_lds(d, tab, rs, out, err, stream))
+    if (d.depthwise && (depthwise_i8_pipe(d, tab, rs, out, err, stream) || depthwise_i8_lds(d, tab, rs, out, err, stream)))
         return;
     if (d.depthwise) {
         DwArgs w{};

@@ -34,6 +34,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lvoid;
+typedef __attribute__((address_space(1))) void gvoid;
 
 struct DwLdsArgs {
     const int8_t* x;
@@ -262,6 +264,263 @@ void launch_epi(const DwLdsArgs& a, unsigned blocks, size_t lds, int ob, bool rs
 #undef TOSA_DW_RC
 }
 
+
+// ---------------------------------------------------------------------------
+// Pipelined variant: persistent workgroups over (image, R output rows, CB
+// channels) tiles. A tile's input rows, its channels' weights and table
+// entries are fetched by direct global -> LDS loads (each load instruction
+// fills 1 KB of LDS from 16-byte pieces: no per-tap scattered reads through
+// the L1) into one of two buffers while the workgroup computes the previous
+// tile from the other. Tiles are numbered channel chunk fastest, then rows,
+// then image; each round of gridDim.x tiles gives every XCD a contiguous run
+// of them, so tiles that share input halo rows or output cache lines meet in
+// one L2.
+struct DwPipeArgs {
+    const int8_t* x;
+    const int8_t* w;
+    const v4i* tab;
+    const int8_t* zfill;  // 16 bytes of the input zero point
+    uint8_t* out;
+    uint32_t* err;
+    int32_t C, IH, IW, OH, OW, KW, KH, T, sy, sx, dy, dx, pt, pl;
+    // Channels per tile and their 16-byte chunks, LDS chunks per position
+    // (nq rounded up to odd: conflict-free fragment reads), tile rows, input
+    // rows and positions per tile, tiles along the height, channel chunks,
+    // tiles in all.
+    int32_t CB, nq, PS, R, HR, HW, tiles_y, nchunks, units;
+    int32_t tslots;  // 16-byte slots of the input rows (HR x HW x PS)
+    int32_t slots;   // slots of a buffer: input, weights [T][CB], table [CB][2]; a multiple of 256
+    FastDiv div_ow, div_hw, div_ps, div_nq, div_nch, div_ty;
+    int32_t zp_w;
+    int32_t clo, chi;
+    int32_t range;
+};
+
+template <int G, int OB, bool RS, bool ZW, bool RC>
+__global__ void __launch_bounds__(256) dw_i8_pipe_kernel(DwPipeArgs A)
+{
+    extern __shared__ v4u s_buf[];  // two buffers of A.slots 16-byte slots
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j16 = lane & 15;
+    const int grp = lane >> 4;
+    // Tile of round k: workgroup b runs on XCD b % 8 and takes place b / 8
+    // of that XCD's run (gridDim.x is a multiple of 8).
+    const int per_xcd = gridDim.x >> 3;
+    const int first = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    auto unit_of = [&](int k) { return k * int(gridDim.x) + first; };
+    auto decode = [&](int u, int& img, int& oy0, int& c0) {
+        const int rest = fdiv(u, A.div_nch);
+        c0 = (u - rest * A.nchunks) * A.CB;
+        img = fdiv(rest, A.div_ty);
+        oy0 = (rest - img * A.tiles_y) * A.R;
+    };
+    // Slot s of a buffer: input chunk (position s / PS, chunk s % PS; chunks
+    // past nq and positions outside the image load the zero-point fill),
+    // then the weights w[t][c0 + 16 q ..], then the table entries of the
+    // tile's channels; slots past those load the fill into padding.
+    auto dma = [&](int u, int buf) {
+        int img, oy0, c0;
+        decode(u, img, oy0, c0);
+        const int iy0 = oy0 * A.sy - A.pt;
+        const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.C + c0;
+        const int wslots = A.T * A.nq;
+        v4u* const dst = s_buf + buf * A.slots;
+        for (int s0 = wave * 64; s0 < A.slots; s0 += 256) {
+            const int s = s0 + lane;
+            const int8_t* src = A.zfill;
+            if (s < A.tslots) {
+                const int hp = fdiv(s, A.div_ps);
+                const int q = s - hp * A.PS;
+                const int hr = fdiv(hp, A.div_hw);
+                const int iy = iy0 + hr, ix = hp - hr * A.HW - A.pl;
+                if (q < A.nq && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW))
+                    src = xi + (int64_t(iy) * A.IW + ix) * A.C + 16 * q;
+            } else if (s < A.tslots + wslots) {
+                const int s2 = s - A.tslots;
+                const int t = fdiv(s2, A.div_nq);
+                src = A.w + t * A.C + c0 + 16 * (s2 - t * A.nq);
+            } else if (s < A.tslots + wslots + 2 * A.CB) {
+                src = reinterpret_cast<const int8_t*>(A.tab + 2 * c0 + (s - A.tslots - wslots));
+            }
+            __builtin_amdgcn_global_load_lds((gvoid*)src, (lvoid*)(dst + s0), 16, 0, 0);
+        }
+    };
+
+    // Tap offsets inside a tile (LDS chunks) of this lane's k-chunk in each
+    // group, and the block-diagonal ones of the weight zero point's term.
+    int32_t toff[G];
+    v4i wo[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int t = 4 * g + grp;
+        const bool tok = t < A.T;
+        const int ky = t / A.KW, kx = t - (t / A.KW) * A.KW;
+        toff[g] = tok ? ((ky * A.dy) * A.HW + kx * A.dx) * A.PS : 0;
+        if constexpr (ZW) {
+            const int sh = 8 * (j16 & 3), wd = j16 >> 2;
+            const uint32_t one = tok ? 1u : 0u;
+            wo[g] = v4i{wd == 0 ? int(one << sh) : 0, wd == 1 ? int(one << sh) : 0, wd == 2 ? int(one << sh) : 0,
+                        wd == 3 ? int(one << sh) : 0};
+        }
+    }
+    uint32_t bad_bits = 0;
+
+    if (first < A.units)
+        dma(first, 0);
+    for (int k = 0;; k++) {
+        const int u = unit_of(k);
+        if (u >= A.units)
+            break;
+        // This tile's loads have landed, and every wave is done with the
+        // buffer that the next tile's loads overwrite.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (unit_of(k + 1) < A.units)
+            dma(unit_of(k + 1), (k + 1) & 1);
+
+        int img, oy0, c0;
+        decode(u, img, oy0, c0);
+        const int rows = A.OH - oy0 < A.R ? A.OH - oy0 : A.R;
+        const int npx = rows * A.OW;
+        const int nblk = (npx + 15) >> 4;
+        const int items = A.nq * nblk;
+        // Items (16-channel block q, 16-pixel block), block major; wave w
+        // takes the w-th quarter, so its fragments change a few times.
+        const int lo = (items * wave) >> 2, hi_item = (items * (wave + 1)) >> 2;
+        const v4u* const sx = s_buf + (k & 1) * A.slots;
+        const uint8_t* const sw = reinterpret_cast<const uint8_t*>(sx + A.tslots);
+        const v4i* const st = reinterpret_cast<const v4i*>(sx + A.tslots + A.T * A.nq);
+        uint8_t* const out0 = A.out + ((int64_t(img) * A.OH + oy0) * A.OW * A.C + c0) * OB;
+        int q = -1, pb = 0;
+        v4i wa[G], t0[4], t1[4];
+        int32_t hi[4];
+        for (int it = lo; it < hi_item; it++) {
+            if (q < 0 || pb == nblk) {
+                q = q < 0 ? it / nblk : q + 1;
+                pb = it - q * nblk;
+                // Block-diagonal weights (byte j16 of 16 is w[t][16 q + j16])
+                // and the table entries of the lane's channels 16 q + 4 grp + i.
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const int t = 4 * g + grp;
+                    const uint32_t wv = t < A.T ? uint32_t(sw[t * A.CB + 16 * q + j16]) : 0u;
+                    const int sh = 8 * (j16 & 3), wd = j16 >> 2;
+                    wa[g] = v4i{wd == 0 ? int(wv << sh) : 0, wd == 1 ? int(wv << sh) : 0,
+                                wd == 2 ? int(wv << sh) : 0, wd == 3 ? int(wv << sh) : 0};
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    t0[i] = st[2 * (16 * q + 4 * grp + i)];
+                    if constexpr (RS)
+                        t1[i] = st[2 * (16 * q + 4 * grp + i) + 1];
+                    hi[i] = ~t0[i].z;
+                }
+            }
+            const int px = 16 * pb + j16;
+            pb++;
+            const bool valid = px < npx;
+            const int pxc = valid ? px : 0;
+            const int r = fdiv(pxc, A.div_ow);
+            const int ox = pxc - r * A.OW;
+            const int base = ((r * A.sy) * A.HW + ox * A.sx) * A.PS + q;
+            v4i acc = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const v4i bx = __builtin_bit_cast(v4i, sx[base + toff[g]]);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, acc, 0, 0, 0);
+                if constexpr (ZW)
+                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc1, 0, 0, 0);
+            }
+            // Result element i of lane (grp, j16): channel 16 q + 4 grp + i
+            // of tile pixel 16 pb + j16.
+            int32_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t xu = uint32_t(acc[i]) + uint32_t(t0[i].x);
+                if constexpr (ZW)
+                    xu += uint32_t(-A.zp_w) * uint32_t(acc1[i]);
+                const int32_t xv = int32_t(xu);
+                if constexpr (RS) {
+                    if constexpr (RC)
+                        bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3_i32(xv, t0[i].z, hi[i])),
+                                                               uint32_t(xv), 0xf6);  // bad | (med3 ^ x)
+                    const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
+                    const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
+                    const int32_t rr = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
+                    v[i] = med3_i32(rr, A.clo, A.chi);  // output zero point folded into rp, rn
+                } else {
+                    v[i] = xv;
+                }
+            }
+            if (valid) {
+                uint8_t* dst = out0 + (int64_t(px) * A.C + 16 * q + 4 * grp) * OB;
+                if constexpr (OB == 1)
+                    *reinterpret_cast<uint32_t*>(dst) = pack4_u8(v[0], v[1], v[2], v[3]);
+                else if constexpr (OB == 2)
+                    *reinterpret_cast<v2u*>(dst) =
+                        v2u{__builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u),
+                            __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u)};
+                else
+                    *reinterpret_cast<v4i*>(dst) = v4i{v[0], v[1], v[2], v[3]};
+            }
+            if constexpr (RS && RC)
+                asm volatile("" : "+v"(bad_bits));
+        }
+    }
+    if (bad_bits)
+        atomicOr(A.err, DERR_SCALE_RANGE);
+}
+
+constexpr int DW_PIPE_BUF_MAX = 32 * 1024;
+
+template <int G, int OB, bool RS, bool ZW, bool RC>
+void launch_pipe(const DwPipeArgs& a, unsigned blocks, size_t lds, hipStream_t s)
+{
+    auto kfn = dw_i8_pipe_kernel<G, OB, RS, ZW, RC>;
+    static bool attr = [&]() {
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      2 * DW_PIPE_BUF_MAX),
+                  "depthwise pipeline LDS size");
+        return true;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(256), lds, s, a);
+}
+
+template <int G>
+void launch_pipe_epi(const DwPipeArgs& a, unsigned blocks, size_t lds, int ob, bool rs, bool zw, hipStream_t s)
+{
+    if (!rs) {
+        if (zw)
+            launch_pipe<G, 4, false, true, false>(a, blocks, lds, s);
+        else
+            launch_pipe<G, 4, false, false, false>(a, blocks, lds, s);
+        return;
+    }
+#define TOSA_DWP_RC(OBV, ZWV)                                      \
+    if (a.range)                                                   \
+        launch_pipe<G, OBV, true, ZWV, true>(a, blocks, lds, s);   \
+    else                                                           \
+        launch_pipe<G, OBV, true, ZWV, false>(a, blocks, lds, s);
+#define TOSA_DWP_OB(OBV)        \
+    if (zw) {                   \
+        TOSA_DWP_RC(OBV, true)  \
+    } else {                    \
+        TOSA_DWP_RC(OBV, false) \
+    }
+    if (ob == 1) {
+        TOSA_DWP_OB(1)
+    } else if (ob == 2) {
+        TOSA_DWP_OB(2)
+    } else {
+        TOSA_DWP_OB(4)
+    }
+#undef TOSA_DWP_OB
+#undef TOSA_DWP_RC
+}
+
 }  // namespace
 
 bool depthwise_i8_lds(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
@@ -336,6 +595,113 @@ bool depthwise_i8_lds(const ConvI8Desc& d, const void* tab, const RescaleDev* rs
         launch_epi<2>(a, unsigned(blocks), lds, ob, rs != nullptr, zw, stream);
     else
         launch_epi<3>(a, unsigned(blocks), lds, ob, rs != nullptr, zw, stream);
+    return true;
+}
+
+bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                       hipStream_t stream)
+{
+    const int T = d.kh * d.kw;
+    const bool aligned = (reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w)) % 16 == 0;
+    if (!d.depthwise || d.ic % 16 != 0 || T > 12 || d.oc != d.ic || !aligned || d.n <= 0 || d.oh <= 0 ||
+        d.ow <= 0)
+        return false;
+    DwPipeArgs a{};
+    const int HW = (d.ow - 1) * d.sx + (d.kw - 1) * d.dx + 1;
+    const int obytes = rs ? rs->out_bytes : 4;
+    // Tile shape: channel chunks CB (a divisor of C in 16-channel steps) and
+    // rows R whose two buffers fit, picked by the bytes the busiest CU
+    // moves: tiles per CU (whole rounds of the persistent grid) x (loaded
+    // input rows + weights + table + written outputs + a fixed cost per
+    // tile). Halo rows count as loaded even where L2 serves them.
+    const long cus = cu_count();
+    const int nch16 = d.ic / 16;
+    long best = -1;
+    for (int nq = 1; nq <= nch16; nq++) {
+        if (nch16 % nq != 0)
+            continue;
+        const int PS = nq | 1;
+        for (int R = 1; R <= d.oh; R++) {
+            const long HR = long(R - 1) * d.sy + long(d.kh - 1) * d.dy + 1;
+            const long tsl = HR * HW * PS;
+            const long slots = (tsl + long(T) * nq + 32L * nq + 255) / 256 * 256;
+            if (slots * 16 > DW_PIPE_BUF_MAX)
+                break;
+            const long wpc = std::min<long>(4, (160L * 1024) / (2 * slots * 16));
+            const long tiles_y = (d.oh + R - 1) / R;
+            const long units = long(d.n) * tiles_y * (nch16 / nq);
+            const long grid = cus * wpc;
+            const long per_cu = (units + grid - 1) / grid * wpc;
+            const long tile_bytes = tsl * 16 + long(R) * d.ow * 16 * nq * obytes + 4096;
+            const long cost = per_cu * tile_bytes;
+            if (best < 0 || cost < best) {
+                best = cost;
+                a.nq = nq;
+                a.R = R;
+            }
+        }
+    }
+    if (best < 0)
+        return false;
+    a.x = d.x;
+    a.w = d.w;
+    a.tab = static_cast<const v4i*>(tab);
+    a.zfill = reinterpret_cast<const int8_t*>(a.tab + 2 * d.oc);
+    a.out = static_cast<uint8_t*>(out);
+    a.err = err;
+    a.C = d.ic;
+    a.IH = d.ih;
+    a.IW = d.iw;
+    a.OH = d.oh;
+    a.OW = d.ow;
+    a.KW = d.kw;
+    a.KH = d.kh;
+    a.T = T;
+    a.sy = d.sy;
+    a.sx = d.sx;
+    a.dy = d.dy;
+    a.dx = d.dx;
+    a.pt = d.pt;
+    a.pl = d.pl;
+    a.zp_w = d.zp_w;
+    int ob = 4;
+    if (rs) {
+        a.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
+        a.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
+        a.range = rs->min_shift <= 31 && !d.range_safe;
+        ob = rs->out_bytes;
+    }
+    a.CB = 16 * a.nq;
+    a.PS = a.nq | 1;
+    a.HR = (a.R - 1) * d.sy + (d.kh - 1) * d.dy + 1;
+    a.HW = HW;
+    a.tiles_y = (d.oh + a.R - 1) / a.R;
+    a.nchunks = d.ic / a.CB;
+    const int64_t units = int64_t(d.n) * a.tiles_y * a.nchunks;
+    if (units >= (int64_t(1) << 30) || int64_t(d.n) * d.ih * d.iw * d.ic >= (int64_t(1) << 40))
+        return false;
+    a.units = int32_t(units);
+    a.tslots = a.HR * a.HW * a.PS;
+    a.slots = (a.tslots + T * a.nq + 2 * a.CB + 255) / 256 * 256;
+    a.div_ow = FastDiv(uint32_t(d.ow));
+    a.div_hw = FastDiv(uint32_t(a.HW));
+    a.div_ps = FastDiv(uint32_t(a.PS));
+    a.div_nq = FastDiv(uint32_t(a.nq));
+    a.div_nch = FastDiv(uint32_t(a.nchunks));
+    a.div_ty = FastDiv(uint32_t(a.tiles_y));
+    const size_t lds = size_t(2) * a.slots * 16;
+    const long wpc = std::min<long>(4, (160L * 1024) / long(lds));
+    // A multiple of 8 workgroups (the tile order deals runs to the 8 XCDs).
+    const int64_t grid = std::min<int64_t>(int64_t(cu_count()) * wpc, (units + 7) / 8 * 8);
+    const unsigned blocks = unsigned((grid + 7) / 8 * 8);
+    const int groups = (T + 3) / 4;
+    const bool zw = d.zp_w != 0;
+    if (groups == 1)
+        launch_pipe_epi<1>(a, blocks, lds, ob, rs != nullptr, zw, stream);
+    else if (groups == 2)
+        launch_pipe_epi<2>(a, blocks, lds, ob, rs != nullptr, zw, stream);
+    else
+        launch_pipe_epi<3>(a, blocks, lds, ob, rs != nullptr, zw, stream);
     return true;
 }
 
