@@ -289,7 +289,7 @@ struct DwPipeArgs {
     // tiles in all.
     int32_t CB, nq, PS, R, HR, HW, tiles_y, nchunks, units;
     int32_t tslots;  // 16-byte slots of the input rows (HR x HW x PS)
-    int32_t slots;   // slots of a buffer: input, weights [T][CB], table [CB][2]; a multiple of 256
+    int32_t slots;   // slots of a buffer: input, weights [T][CB], table [CB][2]; a multiple of 64
     FastDiv div_ow, div_hw, div_ps, div_nq, div_nch, div_ty;
     int32_t zp_w;
     int32_t clo, chi;
@@ -297,7 +297,7 @@ struct DwPipeArgs {
 };
 
 template <int G, int OB, bool RS, bool ZW, bool RC>
-__global__ void __launch_bounds__(256) dw_i8_pipe_kernel(DwPipeArgs A)
+__global__ void __launch_bounds__(512) dw_i8_pipe_kernel(DwPipeArgs A)
 {
     extern __shared__ v4u s_buf[];  // two buffers of A.slots 16-byte slots
     const int tid = threadIdx.x;
@@ -327,7 +327,7 @@ __global__ void __launch_bounds__(256) dw_i8_pipe_kernel(DwPipeArgs A)
         const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.C + c0;
         const int wslots = A.T * A.nq;
         v4u* const dst = s_buf + buf * A.slots;
-        for (int s0 = wave * 64; s0 < A.slots; s0 += 256) {
+        for (int s0 = wave * 64; s0 < A.slots; s0 += 512) {
             const int s = s0 + lane;
             const int8_t* src = A.zfill;
             if (s < A.tslots) {
@@ -384,11 +384,12 @@ __global__ void __launch_bounds__(256) dw_i8_pipe_kernel(DwPipeArgs A)
         decode(u, img, oy0, c0);
         const int rows = A.OH - oy0 < A.R ? A.OH - oy0 : A.R;
         const int npx = rows * A.OW;
-        const int nblk = (npx + 15) >> 4;
+        const int nblk = (npx + 31) >> 5;
         const int items = A.nq * nblk;
-        // Items (16-channel block q, 16-pixel block), block major; wave w
-        // takes the w-th quarter, so its fragments change a few times.
-        const int lo = (items * wave) >> 2, hi_item = (items * (wave + 1)) >> 2;
+        // Items (16-channel block q, 32-pixel block: two independent 16-pixel
+        // MFMA chains), block major; wave w takes the w-th eighth, so its
+        // fragments change a few times.
+        const int lo = (items * wave) >> 3, hi_item = (items * (wave + 1)) >> 3;
         const v4u* const sx = s_buf + (k & 1) * A.slots;
         const uint8_t* const sw = reinterpret_cast<const uint8_t*>(sx + A.tslots);
         const v4i* const st = reinterpret_cast<const v4i*>(sx + A.tslots + A.T * A.nq);
@@ -418,55 +419,65 @@ __global__ void __launch_bounds__(256) dw_i8_pipe_kernel(DwPipeArgs A)
                     hi[i] = ~t0[i].z;
                 }
             }
-            const int px = 16 * pb + j16;
-            pb++;
-            const bool valid = px < npx;
-            const int pxc = valid ? px : 0;
-            const int r = fdiv(pxc, A.div_ow);
-            const int ox = pxc - r * A.OW;
-            const int base = ((r * A.sy) * A.HW + ox * A.sx) * A.PS + q;
-            v4i acc = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
+            int px[2];
+            v4i acc[2], acc1[2];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const v4i bx = __builtin_bit_cast(v4i, sx[base + toff[g]]);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, acc, 0, 0, 0);
-                if constexpr (ZW)
-                    acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc1, 0, 0, 0);
-            }
-            // Result element i of lane (grp, j16): channel 16 q + 4 grp + i
-            // of tile pixel 16 pb + j16.
-            int32_t v[4];
+            for (int b = 0; b < 2; b++) {
+                px[b] = 32 * pb + 16 * b + j16;
+                const int pxc = px[b] < npx ? px[b] : 0;
+                const int r = fdiv(pxc, A.div_ow);
+                const int ox = pxc - r * A.OW;
+                const int base = ((r * A.sy) * A.HW + ox * A.sx) * A.PS + q;
+                acc[b] = v4i{0, 0, 0, 0};
+                acc1[b] = v4i{0, 0, 0, 0};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                uint32_t xu = uint32_t(acc[i]) + uint32_t(t0[i].x);
-                if constexpr (ZW)
-                    xu += uint32_t(-A.zp_w) * uint32_t(acc1[i]);
-                const int32_t xv = int32_t(xu);
-                if constexpr (RS) {
-                    if constexpr (RC)
-                        bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3_i32(xv, t0[i].z, hi[i])),
-                                                               uint32_t(xv), 0xf6);  // bad | (med3 ^ x)
-                    const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
-                    const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
-                    const int32_t rr = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
-                    v[i] = med3_i32(rr, A.clo, A.chi);  // output zero point folded into rp, rn
-                } else {
-                    v[i] = xv;
+                for (int g = 0; g < G; g++) {
+                    const v4i bx = __builtin_bit_cast(v4i, sx[base + toff[g]]);
+                    acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, acc[b], 0, 0, 0);
+                    if constexpr (ZW)
+                        acc1[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc1[b], 0, 0, 0);
                 }
             }
-            if (valid) {
-                uint8_t* dst = out0 + (int64_t(px) * A.C + 16 * q + 4 * grp) * OB;
-                if constexpr (OB == 1)
-                    *reinterpret_cast<uint32_t*>(dst) = pack4_u8(v[0], v[1], v[2], v[3]);
-                else if constexpr (OB == 2)
-                    *reinterpret_cast<v2u*>(dst) =
-                        v2u{__builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u),
-                            __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u)};
-                else
-                    *reinterpret_cast<v4i*>(dst) = v4i{v[0], v[1], v[2], v[3]};
+            pb++;
+            // Result element i of lane (grp, j16) in chain b: channel
+            // 16 q + 4 grp + i of tile pixel 32 pb + 16 b + j16.
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                int32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t xu = uint32_t(acc[b][i]) + uint32_t(t0[i].x);
+                    // |sum of at most 12 input bytes| and |zw| fit 24 bits.
+                    if constexpr (ZW)
+                        xu += uint32_t(__mul24(-A.zp_w, acc1[b][i]));
+                    const int32_t xv = int32_t(xu);
+                    if constexpr (RS) {
+                        if constexpr (RC)
+                            bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3_i32(xv, t0[i].z, hi[i])),
+                                                                   uint32_t(xv), 0xf6);  // bad | (med3 ^ x)
+                        const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
+                        const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
+                        const int32_t rr =
+                            int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
+                        v[i] = med3_i32(rr, A.clo, A.chi);  // output zero point folded into rp, rn
+                    } else {
+                        v[i] = xv;
+                    }
+                }
+                if (px[b] < npx) {
+                    uint8_t* dst = out0 + (int64_t(px[b]) * A.C + 16 * q + 4 * grp) * OB;
+                    if constexpr (OB == 1)
+                        *reinterpret_cast<uint32_t*>(dst) = pack4_u8(v[0], v[1], v[2], v[3]);
+                    else if constexpr (OB == 2)
+                        *reinterpret_cast<v2u*>(dst) =
+                            v2u{__builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u),
+                                __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u)};
+                    else
+                        *reinterpret_cast<v4i*>(dst) = v4i{v[0], v[1], v[2], v[3]};
+                }
+                if constexpr (RS && RC)
+                    asm volatile("" : "+v"(bad_bits));
             }
-            if constexpr (RS && RC)
-                asm volatile("" : "+v"(bad_bits));
         }
     }
     if (bad_bits)
@@ -486,7 +497,7 @@ void launch_pipe(const DwPipeArgs& a, unsigned blocks, size_t lds, hipStream_t s
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(512), lds, s, a);
 }
 
 template <int G>
@@ -624,10 +635,10 @@ bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* r
         for (int R = 1; R <= d.oh; R++) {
             const long HR = long(R - 1) * d.sy + long(d.kh - 1) * d.dy + 1;
             const long tsl = HR * HW * PS;
-            const long slots = (tsl + long(T) * nq + 32L * nq + 255) / 256 * 256;
+            const long slots = (tsl + long(T) * nq + 32L * nq + 63) / 64 * 64;
             if (slots * 16 > DW_PIPE_BUF_MAX)
                 break;
-            const long wpc = std::min<long>(4, (160L * 1024) / (2 * slots * 16));
+            const long wpc = std::min<long>(2, (160L * 1024) / (2 * slots * 16));
             const long tiles_y = (d.oh + R - 1) / R;
             const long units = long(d.n) * tiles_y * (nch16 / nq);
             const long grid = cus * wpc;
@@ -682,7 +693,7 @@ bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* r
         return false;
     a.units = int32_t(units);
     a.tslots = a.HR * a.HW * a.PS;
-    a.slots = (a.tslots + T * a.nq + 2 * a.CB + 255) / 256 * 256;
+    a.slots = (a.tslots + T * a.nq + 2 * a.CB + 63) / 64 * 64;
     a.div_ow = FastDiv(uint32_t(d.ow));
     a.div_hw = FastDiv(uint32_t(a.HW));
     a.div_ps = FastDiv(uint32_t(a.PS));
@@ -690,7 +701,7 @@ bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* r
     a.div_nch = FastDiv(uint32_t(a.nchunks));
     a.div_ty = FastDiv(uint32_t(a.tiles_y));
     const size_t lds = size_t(2) * a.slots * 16;
-    const long wpc = std::min<long>(4, (160L * 1024) / long(lds));
+    const long wpc = std::min<long>(2, (160L * 1024) / long(lds));
     // A multiple of 8 workgroups (the tile order deals runs to the 8 XCDs).
     const int64_t grid = std::min<int64_t>(int64_t(cu_count()) * wpc, (units + 7) / 8 * 8);
     const unsigned blocks = unsigned((grid + 7) / 8 * 8);
