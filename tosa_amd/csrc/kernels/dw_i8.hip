@@ -291,6 +291,9 @@ struct DwPipeArgs {
     int32_t tslots;  // 16-byte slots of the input rows (HR x HW x PS)
     int32_t slots;   // slots of a buffer: input, weights [T][CB], table [CB][2]; a multiple of 64
     FastDiv div_ow, div_hw, div_ps, div_nq, div_nch, div_ty;
+    float inv_ow, hinv_ow;  // 1 / OW and 0.5 / OW (the tile's row of a pixel)
+    int32_t negow;          // -OW
+    int32_t rstep, xstep;   // LDS bytes per output row (16 sy HW PS) and per output column (16 sx PS)
     int32_t zp_w;
     int32_t clo, chi;
     int32_t range;
@@ -348,24 +351,30 @@ __global__ void __launch_bounds__(512) dw_i8_pipe_kernel(DwPipeArgs A)
         }
     };
 
-    // Tap offsets inside a tile (LDS chunks) of this lane's k-chunk in each
-    // group, and the block-diagonal ones of the weight zero point's term.
-    int32_t toff[G];
+    // Tap offsets inside a tile (LDS bytes) of this lane's k-chunk in each
+    // group, and the block-diagonal -zw of the weight zero point's term,
+    // which accumulates into the same chain: sum_t (w - zw) x~.
+    int32_t toff[G];  // bytes
     v4i wo[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const int t = 4 * g + grp;
         const bool tok = t < A.T;
         const int ky = t / A.KW, kx = t - (t / A.KW) * A.KW;
-        toff[g] = tok ? ((ky * A.dy) * A.HW + kx * A.dx) * A.PS : 0;
+        toff[g] = tok ? ((ky * A.dy) * A.HW + kx * A.dx) * A.PS * 16 : 0;
         if constexpr (ZW) {
             const int sh = 8 * (j16 & 3), wd = j16 >> 2;
-            const uint32_t one = tok ? 1u : 0u;
-            wo[g] = v4i{wd == 0 ? int(one << sh) : 0, wd == 1 ? int(one << sh) : 0, wd == 2 ? int(one << sh) : 0,
-                        wd == 3 ? int(one << sh) : 0};
+            const uint32_t nz = tok ? uint32_t(uint8_t(-A.zp_w)) : 0u;  // zw != -128
+            wo[g] = v4i{wd == 0 ? int(nz << sh) : 0, wd == 1 ? int(nz << sh) : 0, wd == 2 ? int(nz << sh) : 0,
+                        wd == 3 ? int(nz << sh) : 0};
         }
     }
     uint32_t bad_bits = 0;
+    // Clamp bounds held in VGPRs for the whole kernel (v_med3 takes one
+    // scalar operand at most).
+    int32_t vclo, vchi;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(vclo) : "s"(A.clo));
+    asm volatile("v_mov_b32 %0, %1" : "=v"(vchi) : "s"(A.chi));
 
     if (first < A.units)
         dma(first, 0);
@@ -395,7 +404,8 @@ __global__ void __launch_bounds__(512) dw_i8_pipe_kernel(DwPipeArgs A)
         const v4i* const st = reinterpret_cast<const v4i*>(sx + A.tslots + A.T * A.nq);
         uint8_t* const out0 = A.out + ((int64_t(img) * A.OH + oy0) * A.OW * A.C + c0) * OB;
         int q = -1, pb = 0;
-        v4i wa[G], t0[4], t1[4];
+        v4i wa[G], t0[4], add;
+        int64_t rp[4], rn[4];
         int32_t hi[4];
         for (int it = lo; it < hi_item; it++) {
             if (q < 0 || pb == nblk) {
@@ -414,28 +424,35 @@ __global__ void __launch_bounds__(512) dw_i8_pipe_kernel(DwPipeArgs A)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     t0[i] = st[2 * (16 * q + 4 * grp + i)];
-                    if constexpr (RS)
-                        t1[i] = st[2 * (16 * q + 4 * grp + i) + 1];
+                    if constexpr (RS) {
+                        const v4i t1 = st[2 * (16 * q + 4 * grp + i) + 1];
+                        rp[i] = __builtin_bit_cast(int64_t, v2i{t1.x, t1.y});
+                        rn[i] = __builtin_bit_cast(int64_t, v2i{t1.z, t1.w});
+                    }
                     hi[i] = ~t0[i].z;
                 }
+                // The chains start at the channels' additive constants.
+                add = v4i{t0[0].x, t0[1].x, t0[2].x, t0[3].x};
             }
+            const char* const sxq = reinterpret_cast<const char*>(sx + q);
             int px[2];
-            v4i acc[2], acc1[2];
+            v4i acc[2];
 #pragma unroll
             for (int b = 0; b < 2; b++) {
                 px[b] = 32 * pb + 16 * b + j16;
                 const int pxc = px[b] < npx ? px[b] : 0;
-                const int r = fdiv(pxc, A.div_ow);
-                const int ox = pxc - r * A.OW;
-                const int base = ((r * A.sy) * A.HW + ox * A.sx) * A.PS + q;
-                acc[b] = v4i{0, 0, 0, 0};
-                acc1[b] = v4i{0, 0, 0, 0};
+                // Row of the tile pixel: pxc / OW rounded down, exact for
+                // pixels below 2^15 and widths up to 4096 (tiles hold fewer
+                // than 2600 pixels).
+                const int r = int(__builtin_fmaf(float(pxc), A.inv_ow, A.hinv_ow));
+                const int ox = __mul24(r, A.negow) + pxc;
+                const int base = __mul24(r, A.rstep) + __mul24(ox, A.xstep);  // bytes
 #pragma unroll
                 for (int g = 0; g < G; g++) {
-                    const v4i bx = __builtin_bit_cast(v4i, sx[base + toff[g]]);
-                    acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, acc[b], 0, 0, 0);
+                    const v4i bx = *reinterpret_cast<const v4i*>(sxq + base + toff[g]);
+                    acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[g], bx, g == 0 ? add : acc[b], 0, 0, 0);
                     if constexpr (ZW)
-                        acc1[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc1[b], 0, 0, 0);
+                        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wo[g], bx, acc[b], 0, 0, 0);
                 }
             }
             pb++;
@@ -446,26 +463,21 @@ __global__ void __launch_bounds__(512) dw_i8_pipe_kernel(DwPipeArgs A)
                 int32_t v[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    uint32_t xu = uint32_t(acc[b][i]) + uint32_t(t0[i].x);
-                    // |sum of at most 12 input bytes| and |zw| fit 24 bits.
-                    if constexpr (ZW)
-                        xu += uint32_t(__mul24(-A.zp_w, acc1[b][i]));
-                    const int32_t xv = int32_t(xu);
+                    const int32_t xv = acc[b][i];
                     if constexpr (RS) {
+                        // (Plain min/max here: the value comes straight from
+                        // the MFMA, whose result hazards the compiler tracks
+                        // only for instructions it emits itself.)
                         if constexpr (RC)
-                            bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3_i32(xv, t0[i].z, hi[i])),
-                                                                   uint32_t(xv), 0xf6);  // bad | (med3 ^ x)
-                        const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
-                        const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
-                        const int32_t rr =
-                            int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp : rn)) >> t0[i].w);
-                        v[i] = med3_i32(rr, A.clo, A.chi);  // output zero point folded into rp, rn
+                            bad_bits |= uint32_t(std::min(std::max(xv, t0[i].z), hi[i]) ^ xv);
+                        const int32_t rr = int32_t((int64_t(xv) * int64_t(t0[i].y) + (xv >= 0 ? rp[i] : rn[i])) >> t0[i].w);
+                        v[i] = med3_i32(rr, vclo, vchi);  // output zero point folded into rp, rn
                     } else {
                         v[i] = xv;
                     }
                 }
                 if (px[b] < npx) {
-                    uint8_t* dst = out0 + (int64_t(px[b]) * A.C + 16 * q + 4 * grp) * OB;
+                    uint8_t* dst = out0 + uint32_t(__mul24(px[b], A.C * OB) + (16 * q + 4 * grp) * OB);
                     if constexpr (OB == 1)
                         *reinterpret_cast<uint32_t*>(dst) = pack4_u8(v[0], v[1], v[2], v[3]);
                     else if constexpr (OB == 2)
@@ -484,7 +496,7 @@ __global__ void __launch_bounds__(512) dw_i8_pipe_kernel(DwPipeArgs A)
         atomicOr(A.err, DERR_SCALE_RANGE);
 }
 
-constexpr int DW_PIPE_BUF_MAX = 32 * 1024;
+constexpr int DW_PIPE_BUF_MAX = 40 * 1024;
 
 template <int G, int OB, bool RS, bool ZW, bool RC>
 void launch_pipe(const DwPipeArgs& a, unsigned blocks, size_t lds, hipStream_t s)
@@ -609,51 +621,19 @@ bool depthwise_i8_lds(const ConvI8Desc& d, const void* tab, const RescaleDev* rs
     return true;
 }
 
-bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
-                       hipStream_t stream)
+namespace {
+
+// Launches the pipelined kernel with tiles of 16 nq channels x R output
+// rows; false when the tile's buffer exceeds the LDS budget.
+bool dw_pipe_launch(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err, int nq,
+                    int R, hipStream_t stream)
 {
     const int T = d.kh * d.kw;
-    const bool aligned = (reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w)) % 16 == 0;
-    if (!d.depthwise || d.ic % 16 != 0 || T > 12 || d.oc != d.ic || !aligned || d.n <= 0 || d.oh <= 0 ||
-        d.ow <= 0)
+    // The weight zero point rides in the MFMA as the int8 -zw.
+    if (nq <= 0 || (d.ic / 16) % nq != 0 || R <= 0 || d.ow > 4096 || d.zp_w == -128)
         return false;
     DwPipeArgs a{};
     const int HW = (d.ow - 1) * d.sx + (d.kw - 1) * d.dx + 1;
-    const int obytes = rs ? rs->out_bytes : 4;
-    // Tile shape: channel chunks CB (a divisor of C in 16-channel steps) and
-    // rows R whose two buffers fit, picked by the bytes the busiest CU
-    // moves: tiles per CU (whole rounds of the persistent grid) x (loaded
-    // input rows + weights + table + written outputs + a fixed cost per
-    // tile). Halo rows count as loaded even where L2 serves them.
-    const long cus = cu_count();
-    const int nch16 = d.ic / 16;
-    long best = -1;
-    for (int nq = 1; nq <= nch16; nq++) {
-        if (nch16 % nq != 0)
-            continue;
-        const int PS = nq | 1;
-        for (int R = 1; R <= d.oh; R++) {
-            const long HR = long(R - 1) * d.sy + long(d.kh - 1) * d.dy + 1;
-            const long tsl = HR * HW * PS;
-            const long slots = (tsl + long(T) * nq + 32L * nq + 63) / 64 * 64;
-            if (slots * 16 > DW_PIPE_BUF_MAX)
-                break;
-            const long wpc = std::min<long>(2, (160L * 1024) / (2 * slots * 16));
-            const long tiles_y = (d.oh + R - 1) / R;
-            const long units = long(d.n) * tiles_y * (nch16 / nq);
-            const long grid = cus * wpc;
-            const long per_cu = (units + grid - 1) / grid * wpc;
-            const long tile_bytes = tsl * 16 + long(R) * d.ow * 16 * nq * obytes + 4096;
-            const long cost = per_cu * tile_bytes;
-            if (best < 0 || cost < best) {
-                best = cost;
-                a.nq = nq;
-                a.R = R;
-            }
-        }
-    }
-    if (best < 0)
-        return false;
     a.x = d.x;
     a.w = d.w;
     a.tab = static_cast<const v4i*>(tab);
@@ -682,6 +662,8 @@ bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* r
         a.range = rs->min_shift <= 31 && !d.range_safe;
         ob = rs->out_bytes;
     }
+    a.nq = nq;
+    a.R = R;
     a.CB = 16 * a.nq;
     a.PS = a.nq | 1;
     a.HR = (a.R - 1) * d.sy + (d.kh - 1) * d.dy + 1;
@@ -694,12 +676,19 @@ bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* r
     a.units = int32_t(units);
     a.tslots = a.HR * a.HW * a.PS;
     a.slots = (a.tslots + T * a.nq + 2 * a.CB + 63) / 64 * 64;
+    if (size_t(a.slots) * 16 > size_t(DW_PIPE_BUF_MAX))
+        return false;
     a.div_ow = FastDiv(uint32_t(d.ow));
     a.div_hw = FastDiv(uint32_t(a.HW));
     a.div_ps = FastDiv(uint32_t(a.PS));
     a.div_nq = FastDiv(uint32_t(a.nq));
     a.div_nch = FastDiv(uint32_t(a.nchunks));
     a.div_ty = FastDiv(uint32_t(a.tiles_y));
+    a.inv_ow = 1.0f / float(d.ow);
+    a.hinv_ow = 0.5f / float(d.ow);
+    a.negow = -d.ow;
+    a.rstep = 16 * d.sy * a.HW * a.PS;
+    a.xstep = 16 * d.sx * a.PS;
     const size_t lds = size_t(2) * a.slots * 16;
     const long wpc = std::min<long>(2, (160L * 1024) / long(lds));
     // A multiple of 8 workgroups (the tile order deals runs to the 8 XCDs).
@@ -714,6 +703,57 @@ bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* r
     else
         launch_pipe_epi<3>(a, blocks, lds, ob, rs != nullptr, zw, stream);
     return true;
+}
+
+
+}  // namespace
+
+bool depthwise_i8_pipe(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                       hipStream_t stream)
+{
+    const int T = d.kh * d.kw;
+    const bool aligned = (reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w)) % 16 == 0;
+    if (!d.depthwise || d.ic % 16 != 0 || T > 12 || d.oc != d.ic || !aligned || d.n <= 0 || d.oh <= 0 ||
+        d.ow <= 0)
+        return false;
+    const int HW = (d.ow - 1) * d.sx + (d.kw - 1) * d.dx + 1;
+    const int obytes = rs ? rs->out_bytes : 4;
+    // Tile shape: channel chunks CB (a divisor of C in 16-channel steps) and
+    // rows R whose two buffers fit, picked by the bytes the busiest CU
+    // moves: tiles per CU (whole rounds of the persistent grid) x (loaded
+    // input rows + weights + table + written outputs + a fixed cost per
+    // tile). Halo rows count as loaded even where L2 serves them.
+    const long cus = cu_count();
+    const int nch16 = d.ic / 16;
+    long best = -1;
+    int bnq = 0, bR = 0;
+    for (int nq = 1; nq <= nch16; nq++) {
+        if (nch16 % nq != 0)
+            continue;
+        const int PS = nq | 1;
+        for (int R = 1; R <= d.oh; R++) {
+            const long HR = long(R - 1) * d.sy + long(d.kh - 1) * d.dy + 1;
+            const long tsl = HR * HW * PS;
+            const long slots = (tsl + long(T) * nq + 32L * nq + 63) / 64 * 64;
+            if (slots * 16 > DW_PIPE_BUF_MAX)
+                break;
+            const long wpc = std::min<long>(2, (160L * 1024) / (2 * slots * 16));
+            const long tiles_y = (d.oh + R - 1) / R;
+            const long units = long(d.n) * tiles_y * (nch16 / nq);
+            const long grid = cus * wpc;
+            const long per_cu = (units + grid - 1) / grid * wpc;
+            const long tile_bytes = tsl * 16 + long(R) * d.ow * 16 * nq * obytes + 4096;
+            const long cost = per_cu * tile_bytes;
+            if (best < 0 || cost < best) {
+                best = cost;
+                bnq = nq;
+                bR = R;
+            }
+        }
+    }
+    if (best < 0)
+        return false;
+    return dw_pipe_launch(d, tab, rs, out, err, bnq, bR, stream);
 }
 
 }  // namespace kern
