@@ -1986,14 +1986,29 @@ void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
             launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
         return;
     }
+    // Over few pixels a pointwise layer's 256-pixel tiles leave most CUs
+    // idle (14 x 14 x 64 images: 49 tiles per channel block); 64-pixel tiles
+    // give four times the workgroups, whose extra weight re-reads hit L2.
+    const int64_t wgs_needed = 2 * int64_t(cu_count());
+    auto few = [&](int64_t bc) { return PW && (int64_t(a.M) + 255) / 256 * ((n + bc - 1) / bc) < wgs_needed; };
     if (w128 <= w32 && w128 <= w16 && n > 64)
         launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s);
-    else if (w64 <= w32 && w64 <= w16 && n > 32)
-        launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
-    else if (w32 <= w16 && n > 16)
-        launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
-    else
-        launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+    else if (w64 <= w32 && w64 <= w16 && n > 32) {
+        if (few(64))
+            launch_epi<64, 64, 1, 4, KC, PW>(a, ob, rs, zw, s);
+        else
+            launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+    } else if (w32 <= w16 && n > 16) {
+        if (few(32))
+            launch_epi<32, 64, 1, 4, KC, PW>(a, ob, rs, zw, s);
+        else
+            launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+    } else {
+        if (few(16))
+            launch_epi<16, 64, 1, 4, KC, PW>(a, ob, rs, zw, s);
+        else
+            launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+    }
 }
 
 constexpr int HALO_LDS_MAX = 160 * 1024;  // LDS of one CU
