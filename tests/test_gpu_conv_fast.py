@@ -576,3 +576,37 @@ def test_pointwise_stream(case):
     clamp = (int(rng.integers(-128, 0)), 100) if case % 3 == 0 else None
     graph, out = build(x, w, bias, zx, zw, [0, 0, 0, 0], [1, 1], [1, 1], rescale=rs, clamp=clamp)
     check(graph, out, {"x": (x, "INT8")})
+
+
+# 3x3 convolutions over 3 input channels with a RESCALE to int8 and at least
+# 4096 output pixels take the stem kernel (im2col built in LDS): strides 1
+# and 2, paddings 0-2 per side, 32-96 output channels.
+STEM = [
+    # n, h, w, stride, (pt, pb, pl, pr), oc
+    (4, 64, 64, 2, (1, 1, 1, 1), 32),
+    (2, 48, 48, 1, (1, 1, 1, 1), 64),
+    (2, 70, 68, 1, (2, 2, 0, 0), 32),
+    (8, 48, 48, 2, (2, 1, 2, 1), 96),
+    (1, 130, 128, 2, (0, 1, 0, 1), 32),
+]
+
+
+@pytest.mark.parametrize("case", range(len(STEM)))
+@pytest.mark.parametrize("zw_on", [False, True])
+def test_stem_conv(case, zw_on):
+    n, h, w_, s, pad, oc = STEM[case]
+    rng = np.random.default_rng(9700 + 2 * case + int(zw_on))
+    pad = list(pad)
+    for d, i in enumerate((h, w_)):
+        full = i - 1 + pad[2 * d] + pad[2 * d + 1] - 2
+        pad[2 * d + 1] -= full % s  # exact output size: trim the far side
+    x = rng.integers(-128, 128, size=(n, h, w_, 3)).astype(np.int8)
+    w = rng.integers(-128, 128, size=(oc, 3, 3, 3)).astype(np.int8)
+    bias = rng.integers(-2 ** 20, 2 ** 20, size=oc).astype(np.int32)
+    zx = int(rng.integers(-128, 128))
+    zw = int(rng.integers(-100, 100)) if zw_on else 0
+    rs = (rng.integers(2 ** 30, 2 ** 31, size=oc), rng.integers(30, 40, size=oc), int(rng.integers(-20, 20)),
+          case % 2 == 0, True)
+    clamp = (0, 100) if case % 2 else None
+    graph, out = build(x, w, bias, zx, zw, pad, [s, s], [1, 1], rescale=rs, clamp=clamp)
+    check(graph, out, {"x": (x, "INT8")})

@@ -151,6 +151,12 @@ void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t
 void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream);
 // Compute units of the current device.
 int cu_count();
+// int8 CONV2D of 3x3 taps over 3 input channels (stride 1 or 2, padding up
+// to 2, iw % 4 == 0, oc % 32 == 0) with the fused RESCALE to int8, its im2col
+// built in LDS (conv_i8.hip); wpad holds the weights as [oc][32] rows (the 27
+// taps, then zeros). False when the shape or epilogue does not fit.
+bool conv_i8_stem(const ConvI8Desc& d, const void* tab, const int8_t* wpad, const RescaleDev* rs, void* out,
+                  uint32_t* err, hipStream_t stream);
 // DEPTHWISE_CONV2D (multiplier 1, ic % 16 == 0, at most 12 taps) over
 // LDS-staged input tiles (dw_i8.hip); false when the shape does not fit its
 // LDS budget. Same table and epilogue contract as conv_i8_fast.

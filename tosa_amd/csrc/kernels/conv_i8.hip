@@ -1900,6 +1900,143 @@ void launch_pws_ta(const PwsArgs& a, hipStream_t s)
         launch_pws<1, KS, ZW>(a, s);
 }
 
+// ---------------------------------------------------------------------------
+// Stem convolution: 3x3 taps over 3 input channels (K = 27 bytes per output
+// pixel), the MobileNet-style first layer, without a materialised im2col. A
+// workgroup owns R output rows of one image and stages the input rows they
+// read in LDS as one 32-bit word per pixel (3 channel bytes, a zero byte), the
+// padding columns and rows holding the input zero point; a global row of 4
+// pixels is 12 bytes, loaded as three words and spread with byte permutes.
+// The 32-byte reduction row of an output pixel in (ky, kx, c) order then is
+// six aligned LDS words -- rows ky = h, h + 1 of the lane's k-half h -- put
+// together with four v_perm_b32 (bytes 27-31 zero, as are the padded weights'
+// there). Weights of 32 channels stay in VGPRs and the epilogue is the
+// streaming pointwise kernel's.
+// ---------------------------------------------------------------------------
+struct StemArgs {
+    const int8_t* x;  // NHWC [n][IH][IW][3]
+    const int8_t* w;  // [N][32]: the 27 weights of a channel, then zeros
+    const v4i* tab;
+    int32_t N, IH, IW, OH, OW, sy, sx, pt, pl;
+    int32_t R, bands, units;  // output rows per workgroup, bands per image, images x bands
+    int32_t HR, WP;           // staged input rows and padded row width (pixels)
+    uint32_t zfw;             // a padding pixel: three zero-point bytes
+    FastDiv div_ow, div_bands, div_g;
+    EpiArgs E;
+};
+
+template <bool ZW>
+__global__ void __launch_bounds__(256, 2) conv_i8_stem_kernel(StemArgs A)
+{
+    extern __shared__ uint32_t s_px[];  // [HR][WP]
+    __shared__ v4i s_tab[2 * 32];
+    __shared__ __attribute__((aligned(16))) int32_t s_add[32];
+    __shared__ int32_t s_rowsum[4][32];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.y * 32;
+
+    for (int i = tid; i < 2 * 32; i += 256) {
+        const int c = n0 + (i >> 1);
+        s_tab[i] = A.tab[2 * (c < A.N ? c : A.N - 1) + (i & 1)];
+    }
+    const int32_t* adds = reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1);
+    for (int i = tid; i < 32; i += 256)
+        s_add[i] = adds[n0 + i < A.N ? n0 + i : A.N - 1];
+    // A fragment: lane (row l32, k-half h) holds bytes 16 h .. + 15 of
+    // channel n0 + h32_row_channel(l32).
+    v4i wa;
+    {
+        const int c = n0 + h32_row_channel(l32);
+        wa = c < A.N ? *reinterpret_cast<const v4i*>(A.w + int64_t(c) * 32 + 16 * h) : v4i{0, 0, 0, 0};
+    }
+    const int groups = A.IW >> 2;  // 4-pixel groups of an input row
+
+    for (int u = blockIdx.x; u < A.units; u += gridDim.x) {
+        const int img = fdiv(u, A.div_bands);
+        const int oy0 = (u - img * A.bands) * A.R;
+        const int rows = A.OH - oy0 < A.R ? A.OH - oy0 : A.R;
+        const int iy0 = oy0 * A.sy - A.pt;
+        __syncthreads();  // the previous band's reads are done
+        // Interior pixels, 4 at a time.
+        for (int i = tid; i < A.HR * groups; i += 256) {
+            const int hr = fdiv(i, A.div_g);
+            const int g = i - hr * groups;
+            const int iy = iy0 + hr;
+            uint32_t* dst = s_px + hr * A.WP + A.pl + 4 * g;
+            if (unsigned(iy) < unsigned(A.IH)) {
+                const uint32_t* src =
+                    reinterpret_cast<const uint32_t*>(A.x + ((int64_t(img) * A.IH + iy) * A.IW + 4 * g) * 3);
+                const uint32_t d0 = src[0], d1 = src[1], d2 = src[2];
+                dst[0] = d0 & 0xffffffu;
+                dst[1] = __builtin_amdgcn_perm(d1, d0, 0x0c050403u);
+                dst[2] = __builtin_amdgcn_perm(d2, d1, 0x0c040302u);
+                dst[3] = d2 >> 8;
+            } else {
+                dst[0] = dst[1] = dst[2] = dst[3] = A.zfw;
+            }
+        }
+        // Padding columns left and right of the image.
+        const int pr = A.WP - A.pl - A.IW;
+        for (int i = tid; i < A.HR * (A.pl + pr); i += 256) {
+            const int hr = i / (A.pl + pr);
+            const int c = i - hr * (A.pl + pr);
+            s_px[hr * A.WP + (c < A.pl ? c : A.IW + c)] = A.zfw;
+        }
+        __syncthreads();
+
+        const int npx = rows * A.OW;
+        const int ntl = (npx + 31) >> 5;
+        const int64_t m0 = (int64_t(img) * A.OH + oy0) * A.OW;
+        for (int t = wave; t < ntl; t += 4) {
+            const int p = 32 * t + l32;
+            const int pc = p < npx ? p : 0;
+            const int r = fdiv(pc, A.div_ow);
+            const int ox = pc - r * A.OW;
+            // Words of taps (h, 0..2) and (h + 1, 0..2).
+            const uint32_t* q = s_px + (r * A.sy + h) * A.WP + ox * A.sx;
+            const uint32_t a0 = q[0], a1 = q[1], a2 = q[2];
+            const uint32_t b0 = q[A.WP], b1 = q[A.WP + 1], b2 = q[A.WP + 2];
+            v4i fb;
+            if (h == 0) {
+                fb = v4i{int(__builtin_amdgcn_perm(a1, a0, 0x04020100u)), int(__builtin_amdgcn_perm(a2, a1, 0x05040201u)),
+                         int(__builtin_amdgcn_perm(b0, a2, 0x06050402u)), int(__builtin_amdgcn_perm(b2, b1, 0x04020100u))};
+            } else {
+                fb = v4i{int(__builtin_amdgcn_perm(b0, a2, 0x05040201u)), int(__builtin_amdgcn_perm(b1, b0, 0x06050402u)),
+                         int(b2), 0};
+            }
+            if constexpr (ZW) {
+                int32_t sxs = 0;
+                sxs = __builtin_amdgcn_sdot4(fb.x, 0x01010101, sxs, false);
+                sxs = __builtin_amdgcn_sdot4(fb.y, 0x01010101, sxs, false);
+                sxs = __builtin_amdgcn_sdot4(fb.z, 0x01010101, sxs, false);
+                sxs = __builtin_amdgcn_sdot4(fb.w, 0x01010101, sxs, false);
+                sxs += __shfl_xor(sxs, 32);
+                if (h == 0)
+                    s_rowsum[wave][l32] = sxs;
+                __builtin_amdgcn_wave_barrier();
+            }
+            v16i acc[1][1];
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const v4i v = *reinterpret_cast<const v4i*>(s_add + 16 * h + 4 * qd);
+                acc[0][0][4 * qd] = v.x;
+                acc[0][0][4 * qd + 1] = v.y;
+                acc[0][0][4 * qd + 2] = v.z;
+                acc[0][0][4 * qd + 3] = v.w;
+            }
+            acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa, fb, acc[0][0], 0, 0, 0);
+            const int p0 = 32 * t;
+            epilogue32<1, 1, 1, 1, true, ZW>(acc, s_tab, s_rowsum[wave], n0, 0, lane, A.E,
+                                            [&](int pp) { return p0 + pp < npx ? m0 + p0 + pp : int64_t(-1); });
+            if constexpr (ZW)
+                __builtin_amdgcn_wave_barrier();  // the row sums are read before the next tile's
+        }
+    }
+}
+
 // The streaming pointwise kernel takes 1x1 stride-1 convolutions with
 // K = ic a multiple of 16 up to 64, N a multiple of 32 (its epilogue works on
 // whole 32-channel tiles: with N = 16, 24 or 144 the padded channels made it
@@ -2306,6 +2443,63 @@ void launch_dw_epi(const DwArgs& a, int ob, bool rs, bool zw, hipStream_t s)
 }
 
 }  // namespace
+
+bool conv_i8_stem(const ConvI8Desc& d, const void* tab, const int8_t* wpad, const RescaleDev* rs, void* out,
+                  uint32_t* err, hipStream_t stream)
+{
+    if (!rs || rs->out_bytes != 1 || !conv_i8_fast_epilogue_ok(*rs) || d.depthwise || d.batch != 1 || d.ic != 3 ||
+        d.kh != 3 || d.kw != 3 || d.dy != 1 || d.dx != 1 || d.iw % 4 != 0 || d.sy < 1 || d.sy > 2 || d.sx < 1 ||
+        d.sx > 2 || d.pt < 0 || d.pt > 2 || d.pl < 0 || d.pl > 2 || d.oc % 32 != 0 ||
+        reinterpret_cast<uintptr_t>(d.x) % 4 != 0 || reinterpret_cast<uintptr_t>(wpad) % 16 != 0 ||
+        int64_t(d.n) * d.oh * d.ow < 4096 || int64_t(d.n) * d.ih * d.iw * 3 >= (int64_t(1) << 31))
+        return false;
+    StemArgs a{};
+    a.WP = (d.ow - 1) * d.sx + 3;
+    if (a.WP < d.pl + d.iw)
+        return false;  // the image's own columns must all be staged
+    a.x = d.x;
+    a.w = wpad;
+    a.tab = static_cast<const v4i*>(tab);
+    a.N = d.oc;
+    a.IH = d.ih;
+    a.IW = d.iw;
+    a.OH = d.oh;
+    a.OW = d.ow;
+    a.sy = d.sy;
+    a.sx = d.sx;
+    a.pt = d.pt;
+    a.pl = d.pl;
+    // Rows per band: staged rows within 32 KB of LDS, and bands enough for
+    // four workgroups per CU.
+    int R = std::max(1, std::min(d.oh, ((32 * 1024) / (4 * a.WP) - 3) / d.sy + 1));
+    while (R > 1 && int64_t(d.n) * ((d.oh + R - 1) / R) < 4 * int64_t(cu_count()))
+        R = (R + 1) / 2;
+    a.R = R;
+    a.bands = (d.oh + R - 1) / R;
+    a.units = d.n * a.bands;
+    a.HR = (R - 1) * d.sy + 3;
+    a.zfw = (uint32_t(uint8_t(d.zp_x)) * 0x010101u);
+    a.div_ow = FastDiv(uint32_t(d.ow));
+    a.div_bands = FastDiv(uint32_t(a.bands));
+    a.div_g = FastDiv(uint32_t(d.iw / 4));
+    EpiArgs& e = a.E;
+    e.out = static_cast<uint8_t*>(out);
+    e.N = d.oc;
+    e.zp_w = d.zp_w;
+    e.err = err;
+    e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
+    e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
+    e.range = rs->min_shift <= 31 && !d.range_safe;
+    const size_t lds = size_t(a.HR) * a.WP * 4;
+    if (lds > 64 * 1024)
+        return false;
+    const dim3 grid(unsigned(a.units), unsigned(d.oc / 32));
+    if (d.zp_w != 0)
+        hipLaunchKernelGGL(conv_i8_stem_kernel<true>, grid, dim3(256), lds, stream, a);
+    else
+        hipLaunchKernelGGL(conv_i8_stem_kernel<false>, grid, dim3(256), lds, stream, a);
+    return true;
+}
 
 bool conv_i8_fast_supported(const ConvI8Desc& d)
 {

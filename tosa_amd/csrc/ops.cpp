@@ -910,6 +910,13 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
                                      w_const, s, [&](void* dst) {
                                          conv_i8_rowpad(fd.w, fd.oc, K, kp, static_cast<int8_t*>(dst), s);
                                      });
+                if (kp == 32) {
+                    // A 3-channel 3x3 stem: the im2col is built in LDS.
+                    ConvI8Desc sd = fd;
+                    sd.range_safe = tab->scale_range_safe;
+                    if (conv_i8_stem(sd, tab->device_in(), static_cast<const int8_t*>(wp->device_in()), rs, out, err, s))
+                        return;
+                }
                 auto xcol = make_device_storage(DT_INT8, int64_t(fd.n) * fd.oh * fd.ow * kp);
                 conv_i8_im2col(fd, static_cast<int8_t*>(xcol->device_out()), s);
                 ConvI8Desc p = fd;
