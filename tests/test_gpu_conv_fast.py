@@ -542,8 +542,8 @@ def test_range_bound_runtime_bias(case):
 # channel-tile count (TA 1-4, and N past 128 in several blocks), one and two
 # reduction steps (K = 16 and 48 leave a zero-filled half step), nonzero
 # weight zero points, shifts below 32 (range check live), a fused CLAMP and
-# pixel counts that are not a multiple of 32; the last case (N = 24) stays
-# on the tiled kernel.
+# pixel counts that are not a multiple of 32; (N = 24, K = 32) stays on the
+# tiled kernel. K % 16 == 8 cases read each row as 8-byte halves.
 PWS = [
     # n, h, w, ic, oc
     (1, 64, 64, 16, 96),
@@ -554,6 +554,11 @@ PWS = [
     (2, 50, 41, 16, 128),
     (1, 80, 80, 64, 160),
     (2, 48, 47, 32, 24),
+    # K % 16 == 8: 8-byte row halves, N a multiple of 16 in one-tile blocks
+    (2, 48, 47, 24, 144),
+    (1, 70, 64, 40, 48),
+    (1, 64, 66, 56, 16),
+    (3, 40, 40, 24, 32),
 ]
 
 

@@ -151,6 +151,11 @@ void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t
 void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream);
 // Compute units of the current device.
 int cu_count();
+// 1x1 stride-1 int8 CONV2D with the fused RESCALE to int8 on the streaming
+// pointwise kernel, for the shapes it takes (conv_i8.hip: K <= 64 a multiple
+// of 8, many pixels); false otherwise.
+bool conv_i8_pointwise_stream(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                              hipStream_t stream);
 // int8 CONV2D of 3x3 taps over 3 input channels (stride 1 or 2, padding up
 // to 2, iw % 4 == 0, oc % 32 == 0) with the fused RESCALE to int8, its im2col
 // built in LDS (conv_i8.hip); wpad holds the weights as [oc][32] rows (the 27

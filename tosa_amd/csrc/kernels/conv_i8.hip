@@ -1306,6 +1306,8 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 // KS v_mfma_i32_32x32x32_i8, and the 32x32 epilogue. Reduction bytes past K
 // load as zeros on both sides, so they add nothing to the dot products or to
 // the weight zero point's per-pixel sums; the table's terms use the real K.
+// K8: K % 16 == 8 (rows 8-byte aligned), every 16-byte piece loads as two
+// 8-byte halves, each only where it lies inside the row.
 // ---------------------------------------------------------------------------
 struct PwsArgs {
     const int8_t* x;  // [M][K]
@@ -1316,9 +1318,19 @@ struct PwsArgs {
     EpiArgs E;
 };
 
-template <int TA, int KS, int OB, bool RS, bool ZW>
+template <int TA, int KS, int OB, bool RS, bool ZW, bool K8>
 __global__ void __launch_bounds__(256, 2) conv_i8_pws_kernel(PwsArgs A)
 {
+    // 16 bytes of a row at byte k, zeros past K.
+    auto ld_piece = [&](const int8_t* row, int k) -> v4i {
+        if constexpr (!K8) {
+            return k < A.K ? *reinterpret_cast<const v4i*>(row + k) : v4i{0, 0, 0, 0};
+        } else {
+            const v2i lo = k + 8 <= A.K ? *reinterpret_cast<const v2i*>(row + k) : v2i{0, 0};
+            const v2i hi = k + 16 <= A.K ? *reinterpret_cast<const v2i*>(row + k + 8) : v2i{0, 0};
+            return v4i{lo.x, lo.y, hi.x, hi.y};
+        }
+    };
     __shared__ v4i s_tab[2 * 32 * TA];
     __shared__ __attribute__((aligned(16))) int32_t s_add[32 * TA];  // additive constants
     __shared__ int32_t s_rowsum[4][32];
@@ -1345,7 +1357,7 @@ __global__ void __launch_bounds__(256, 2) conv_i8_pws_kernel(PwsArgs A)
 #pragma unroll
         for (int j = 0; j < KS; j++) {
             const int k = 32 * j + 16 * h;
-            wa[a][j] = (c < A.N && k < A.K) ? *reinterpret_cast<const v4i*>(A.w + int64_t(c) * A.K + k) : v4i{0, 0, 0, 0};
+            wa[a][j] = c < A.N ? ld_piece(A.w + int64_t(c) * A.K, k) : v4i{0, 0, 0, 0};
         }
     }
     __syncthreads();
@@ -1357,7 +1369,7 @@ __global__ void __launch_bounds__(256, 2) conv_i8_pws_kernel(PwsArgs A)
 #pragma unroll
         for (int j = 0; j < KS; j++) {
             const int k = 32 * j + 16 * h;
-            fb[j] = (p < A.M && k < A.K) ? *reinterpret_cast<const v4i*>(A.x + int64_t(p) * A.K + k) : v4i{0, 0, 0, 0};
+            fb[j] = p < A.M ? ld_piece(A.x + int64_t(p) * A.K, k) : v4i{0, 0, 0, 0};
         }
     };
     v4i fb[KS], fn[KS];
@@ -1877,19 +1889,24 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
                          int32_t(uint32_t(uint64_t(rn))), int32_t(uint64_t(rn) >> 32)};
 }
 
-template <int TA, int KS, bool ZW>
+template <int TA, int KS, bool ZW, bool K8 = false>
 void launch_pws(const PwsArgs& a, hipStream_t s)
 {
     const unsigned wgs = unsigned(std::min<int64_t>((a.ntiles + 3) / 4, int64_t(2) * cu_count()));
-    hipLaunchKernelGGL((conv_i8_pws_kernel<TA, KS, 1, true, ZW>), dim3(wgs, unsigned((a.N + 32 * TA - 1) / (32 * TA))),
-                       dim3(256), 0, s, a);
+    hipLaunchKernelGGL((conv_i8_pws_kernel<TA, KS, 1, true, ZW, K8>),
+                       dim3(wgs, unsigned((a.N + 32 * TA - 1) / (32 * TA))), dim3(256), 0, s, a);
 }
 
-// Channel tiles per block: the most of 4, 3, 2, 1 that divide N / 32.
+// Channel tiles per block: the most of 4, 3, 2, 1 that divide N / 32 (one,
+// the last partial, when N is not a multiple of 32).
 template <int KS, bool ZW>
 void launch_pws_ta(const PwsArgs& a, hipStream_t s)
 {
     const int t = a.N / 32;
+    if (a.K % 16 == 8) {
+        launch_pws<1, KS, ZW, true>(a, s);
+        return;
+    }
     if (t % 4 == 0)
         launch_pws<4, KS, ZW>(a, s);
     else if (t % 3 == 0)
@@ -2041,12 +2058,17 @@ __global__ void __launch_bounds__(256, 2) conv_i8_stem_kernel(StemArgs A)
 // K = ic a multiple of 16 up to 64, N a multiple of 32 (its epilogue works on
 // whole 32-channel tiles: with N = 16, 24 or 144 the padded channels made it
 // no faster than the tiled kernel), many pixels (its persistent waves need
-// tiles to walk) and the fused RESCALE to int8.
+// tiles to walk) and the fused RESCALE to int8. With K % 16 == 8 (24, 40,
+// 56 channels: otherwise an im2col pad copy and the tiled kernel) it also
+// takes N a multiple of 16, in one-tile channel blocks.
 bool pws_applies(const ConvI8Desc& d, bool pw, int ob, const RescaleDev* rs)
 {
     const int64_t m = int64_t(d.n) * d.oh * d.ow;
-    return pw && d.batch == 1 && rs && ob == 1 && d.ic % 16 == 0 && d.ic <= 64 && d.oc % 32 == 0 && m >= 4096 &&
-           m * d.ic < (int64_t(1) << 31) && (reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w)) % 16 == 0;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(d.x) | reinterpret_cast<uintptr_t>(d.w);
+    const bool k16 = d.ic % 16 == 0 && d.oc % 32 == 0 && al % 16 == 0;
+    const bool k8 = d.ic % 16 == 8 && d.oc % 16 == 0 && al % 8 == 0;
+    return pw && d.batch == 1 && rs && ob == 1 && (k16 || k8) && d.ic <= 64 && m >= 4096 &&
+           m * d.ic < (int64_t(1) << 31);
 }
 
 template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW>
@@ -2443,6 +2465,44 @@ void launch_dw_epi(const DwArgs& a, int ob, bool rs, bool zw, hipStream_t s)
 }
 
 }  // namespace
+
+bool conv_i8_pointwise_stream(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
+                              hipStream_t stream)
+{
+    const bool pw = !d.depthwise && d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 &&
+                    d.ih == d.oh && d.iw == d.ow;
+    if (!rs || !conv_i8_fast_epilogue_ok(*rs) || !pws_applies(d, pw, rs->out_bytes, rs))
+        return false;
+    PwsArgs a{};
+    a.x = d.x;
+    a.w = d.w;
+    a.tab = static_cast<const v4i*>(tab);
+    a.M = d.n * d.oh * d.ow;
+    a.K = d.ic;
+    a.N = d.oc;
+    a.ntiles = (a.M + 31) / 32;
+    EpiArgs& e = a.E;
+    e.out = static_cast<uint8_t*>(out);
+    e.N = d.oc;
+    e.zp_w = d.zp_w;
+    e.err = err;
+    e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
+    e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
+    e.range = rs->min_shift <= 31 && !d.range_safe;
+    const bool zw = d.zp_w != 0;
+    if (d.ic <= 32) {
+        if (zw)
+            launch_pws_ta<1, true>(a, stream);
+        else
+            launch_pws_ta<1, false>(a, stream);
+    } else {
+        if (zw)
+            launch_pws_ta<2, true>(a, stream);
+        else
+            launch_pws_ta<2, false>(a, stream);
+    }
+    return true;
+}
 
 bool conv_i8_stem(const ConvI8Desc& d, const void* tab, const int8_t* wpad, const RescaleDev* rs, void* out,
                   uint32_t* err, hipStream_t stream)

@@ -905,6 +905,14 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
                 // Channels or geometry the tiled kernels do not take: a
                 // pointwise GEMM over the materialised im2col.
                 auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), rs, wb_const && (!rs || rs_const), s);
+                {
+                    // A 1x1 convolution over 8 mod 16 channels: the streaming
+                    // pointwise kernel reads the rows as they are.
+                    ConvI8Desc sd = fd;
+                    sd.range_safe = tab->scale_range_safe;
+                    if (conv_i8_pointwise_stream(sd, tab->device_in(), rs, out, err, s))
+                        return;
+                }
                 const int32_t K = fd.kh * fd.kw * fd.ic, kp = conv_i8_im2col_kp(fd);
                 auto wp = derived_i8(*weight->data, "conv_i8_rowpad:" + std::to_string(kp), int64_t(fd.oc) * kp,
                                      w_const, s, [&](void* dst) {
