@@ -1897,14 +1897,21 @@ void launch_pws(const PwsArgs& a, hipStream_t s)
                        dim3(wgs, unsigned((a.N + 32 * TA - 1) / (32 * TA))), dim3(256), 0, s, a);
 }
 
-// Channel tiles per block: the most of 4, 3, 2, 1 that divide N / 32 (one,
-// the last partial, when N is not a multiple of 32).
+// Channel tiles per block: the most of 4, 3, 2, 1 that divide N / 32 (with
+// K % 16 == 8, up to three and the last block partial).
 template <int KS, bool ZW>
 void launch_pws_ta(const PwsArgs& a, hipStream_t s)
 {
     const int t = a.N / 32;
     if (a.K % 16 == 8) {
-        launch_pws<1, KS, ZW, true>(a, s);
+        // Up to three 32-channel tiles per block (the last block partial).
+        const int tiles = (a.N + 31) / 32;
+        if (tiles >= 3)
+            launch_pws<3, KS, ZW, true>(a, s);
+        else if (tiles == 2)
+            launch_pws<2, KS, ZW, true>(a, s);
+        else
+            launch_pws<1, KS, ZW, true>(a, s);
         return;
     }
     if (t % 4 == 0)
@@ -2879,7 +2886,12 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     a.bso = int64_t(a.M) * a.N * ob;
     a.bst = int32_t(conv_i8_table_stride(d.oc) / 4);
     if (pw) {
-        if (a.K >= 128)
+        // 128-byte reduction steps, except for 128 < K < 192, where 64-byte
+        // ones stage a quarter fewer bytes (K = 144: 192 per row instead of
+        // 256; 144 -> 24 at 56 x 56: 18.3 -> 13.6 us). For longer K the extra
+        // steps cost more than the padding (K = 960 over 7 x 7 images: 3-4 us
+        // slower with 64).
+        if (a.K >= 192 || a.K == 128)
             launch_tile<128, true>(a, ob, rs != nullptr, zw, stream);
         else
             launch_tile<64, true>(a, ob, rs != nullptr, zw, stream);
