@@ -55,9 +55,11 @@ struct FusionPlan {
 class ExecState {
 public:
     const BasicBlock* block = nullptr;
+    using DefMap = std::unordered_map<std::string, const TensorDef*>;
     std::unordered_map<std::string, TensorPtr> tensors;
-    std::unordered_map<std::string, const TensorDef*> defs;
-    std::unordered_map<std::string, const TensorDef*> const_defs;  // outputs of CONST ops
+    // Built once per graph by the Interpreter and shared by its runs.
+    const DefMap* defs = nullptr;
+    const DefMap* const_defs = nullptr;  // outputs of CONST ops
     ConstCache* consts = nullptr;
     const FusionPlan* plan = nullptr;
     RunOptions opts;
@@ -68,6 +70,7 @@ public:
     TensorPtr get(const std::string& name) const;  // Error(ERR_TENSOR_NOT_FOUND)
     void set(const TensorPtr& t) { tensors[t->name] = t; }
     const TensorDef* find_def(const std::string& name) const;
+    bool is_const(const std::string& name) const { return const_defs->count(name) != 0; }
     // An operand of a consumer that has not run yet: a present tensor or a
     // CONST output (decoded from the graph); null otherwise.
     TensorPtr resolve(const std::string& name) const;

@@ -16,8 +16,6 @@
 #include <algorithm>
 #include <cstdlib>
 #include <deque>
-#include <set>
-#include <unordered_set>
 
 namespace tosa {
 
@@ -111,10 +109,95 @@ FusionPlan FusionPlan::build(const BasicBlock& b)
 // ---------------------------------------------------------------------------
 // Interpreter
 // ---------------------------------------------------------------------------
-Interpreter::Interpreter(Graph graph) : graph_(std::move(graph)), consts_(new ConstCache())
+BlockIndex BlockIndex::build(const BasicBlock& b)
 {
-    if (const BasicBlock* b = graph_.main_block())
+    BlockIndex x;
+    for (const auto& td : b.tensors)
+        x.defs[td.name] = &td;
+    for (const auto& o : b.operators)
+        if ((o.op == OP_CONST || o.op == OP_CONST_SHAPE) && !o.outputs.empty()) {
+            auto it = x.defs.find(o.outputs[0]);
+            if (it != x.defs.end())
+                x.const_defs[o.outputs[0]] = it->second;
+        }
+    // Rank check (src/interpreter.rs:157-163): the first offending tensor.
+    for (const auto& t : b.tensors)
+        if (t.dtype != DT_SHAPE && t.shape.size() > MAX_RANK) {
+            x.rank_error = "tensor '" + t.name + "' has rank " + std::to_string(t.shape.size()) +
+                           ", above the maximum of " + std::to_string(MAX_RANK);
+            break;
+        }
+    auto id_of = [&x](const std::string& name) {
+        auto it = x.ids.emplace(name, int(x.ids.size())).first;
+        return it->second;
+    };
+    const size_t n = b.operators.size();
+    x.op_inputs.resize(n);
+    x.op_outputs.resize(n);
+    for (size_t i = 0; i < n; i++) {
+        const Operator& o = b.operators[i];
+        if (o.op != OP_CONST) {
+            for (const auto& name : o.inputs)
+                x.op_inputs[i].push_back(id_of(name));
+            std::sort(x.op_inputs[i].begin(), x.op_inputs[i].end());
+            x.op_inputs[i].erase(std::unique(x.op_inputs[i].begin(), x.op_inputs[i].end()), x.op_inputs[i].end());
+        }
+        for (const auto& name : o.outputs)
+            x.op_outputs[i].push_back(id_of(name));
+    }
+    return x;
+}
+
+Interpreter::Interpreter(Graph graph)
+    : graph_(std::move(graph)), consts_(new ConstCache()), sched_(new ScheduleCache())
+{
+    if (const BasicBlock* b = graph_.main_block()) {
         plan_ = FusionPlan::build(*b);
+        index_ = BlockIndex::build(*b);
+    }
+}
+
+// The schedule for this run's input names: the last one built when the names
+// are the same (the usual case of repeated runs), else a new one.
+std::shared_ptr<const Schedule> Interpreter::schedule_for(const TensorMap& inputs) const
+{
+    {
+        std::lock_guard<std::mutex> lk(sched_->mu);
+        const auto& last = sched_->last;
+        if (last && last->input_names.size() == inputs.size()) {
+            bool same = true;
+            for (const auto& kv : inputs)
+                if (!last->input_names.count(kv.first)) {
+                    same = false;
+                    break;
+                }
+            if (same)
+                return last;
+        }
+    }
+    auto s = std::make_shared<Schedule>();
+    const size_t n = index_.op_inputs.size();
+    s->available.assign(index_.ids.size(), 0);
+    for (const auto& kv : inputs) {
+        s->input_names.insert(kv.first);
+        auto it = index_.ids.find(kv.first);
+        if (it != index_.ids.end())
+            s->available[it->second] = 1;
+    }
+    s->missing.assign(n, 0);
+    s->waiting.resize(index_.ids.size());
+    for (size_t i = 0; i < n; i++)
+        for (int id : index_.op_inputs[i])
+            if (!s->available[id]) {
+                s->missing[i]++;
+                s->waiting[id].push_back(i);
+            }
+    for (size_t i = 0; i < n; i++)
+        if (s->missing[i] == 0)
+            s->queue.push_back(i);
+    std::lock_guard<std::mutex> lk(sched_->mu);
+    sched_->last = s;
+    return s;
 }
 
 Interpreter Interpreter::from_flatbuffer(const uint8_t* data, size_t len)
@@ -135,12 +218,8 @@ TensorMap Interpreter::run(const TensorMap& inputs, InterpreterHook& hook, const
 
     ExecState st;
     st.block = block;
-    for (const auto& td : block->tensors)
-        st.defs[td.name] = &td;
-    for (const auto& o : block->operators)
-        if ((o.op == OP_CONST || o.op == OP_CONST_SHAPE) && !o.outputs.empty())
-            if (const TensorDef* d = st.find_def(o.outputs[0]))
-                st.const_defs[o.outputs[0]] = d;
+    st.defs = &index_.defs;
+    st.const_defs = &index_.const_defs;
     st.tensors = inputs;
     st.consts = consts_.get();
     st.plan = &plan_;
@@ -148,37 +227,21 @@ TensorMap Interpreter::run(const TensorMap& inputs, InterpreterHook& hook, const
     if (hook.reads_data())
         st.opts.fusion = false;  // every intermediate is materialised for such a hook
 
-    // Rank check (src/interpreter.rs:157-163).
-    for (const auto& t : block->tensors)
-        if (t.dtype != DT_SHAPE && t.shape.size() > MAX_RANK)
-            throw Error(ERR_SHAPE_MISMATCH, "tensor '" + t.name + "' has rank " + std::to_string(t.shape.size()) +
-                                                ", above the maximum of " + std::to_string(MAX_RANK));
+    if (!index_.rank_error.empty())
+        throw Error(ERR_SHAPE_MISMATCH, index_.rank_error);
 
     const auto& ops = block->operators;
     const size_t n = ops.size();
-    // Distinct input names per operator, and their consumers.
-    std::unordered_set<std::string> available;
-    for (const auto& kv : st.tensors)
-        available.insert(kv.first);
-    std::unordered_map<std::string, std::vector<size_t>> waiting;  // name -> ops missing it
-    std::vector<size_t> missing(n, 0);
-    for (size_t i = 0; i < n; i++) {
-        if (ops[i].op == OP_CONST)
-            continue;
-        std::set<std::string> distinct(ops[i].inputs.begin(), ops[i].inputs.end());
-        for (const auto& name : distinct)
-            if (!available.count(name)) {
-                missing[i]++;
-                waiting[name].push_back(i);
-            }
-    }
+    // Count of distinct input names each operator still misses, and the
+    // consumers of each name (the part that depends only on the graph and the
+    // input names is built once and copied here).
+    const std::shared_ptr<const Schedule> sched = schedule_for(inputs);
+    std::vector<char> available = sched->available;
+    std::vector<size_t> missing = sched->missing;
     std::vector<bool> executed(n, false), queued(n, false);
-    std::deque<size_t> queue;
-    for (size_t i = 0; i < n; i++)
-        if (missing[i] == 0) {
-            queue.push_back(i);
-            queued[i] = true;
-        }
+    std::deque<size_t> queue(sched->queue.begin(), sched->queue.end());
+    for (size_t i : sched->queue)
+        queued[i] = true;
 
     const bool sync_each = !hook.is_noop() && hook.needs_sync();
     const bool noop = hook.is_noop();
@@ -227,13 +290,11 @@ TensorMap Interpreter::run(const TensorMap& inputs, InterpreterHook& hook, const
         ops_executed++;
         // Newly available outputs release waiting operators, in graph order.
         std::vector<size_t> ready;
-        for (const auto& name : op.outputs) {
-            if (!available.insert(name).second)
+        for (int id : index_.op_outputs[idx]) {
+            if (available[id])
                 continue;
-            auto w = waiting.find(name);
-            if (w == waiting.end())
-                continue;
-            for (size_t j : w->second)
+            available[id] = 1;
+            for (size_t j : sched->waiting[id])
                 if (--missing[j] == 0 && !executed[j] && !queued[j])
                     ready.push_back(j);
         }

@@ -4,8 +4,11 @@
 #pragma once
 
 #include <memory>
+#include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
+#include <vector>
 
 #include "exec.h"
 #include "hooks.h"
@@ -17,6 +20,29 @@ using TensorMap = std::unordered_map<std::string, TensorPtr>;
 
 // Highest tensor rank supported (src/interpreter.rs:150-152).
 constexpr size_t MAX_RANK = 6;
+
+// What every run of one block shares, built once per graph: the tensor
+// definitions by name, a dense id per operand/result name, and each
+// operator's distinct input ids and output ids.
+struct BlockIndex {
+    ExecState::DefMap defs, const_defs;
+    std::string rank_error;  // non-empty: the block holds a tensor above MAX_RANK
+    std::unordered_map<std::string, int> ids;
+    std::vector<std::vector<int>> op_inputs;   // distinct, per operator (empty for CONST)
+    std::vector<std::vector<int>> op_outputs;  // in operand order, per operator
+    static BlockIndex build(const BasicBlock& b);
+};
+
+// The ready queue's starting state for one set of input names: which ids are
+// available, how many distinct inputs each operator still misses, the
+// operators waiting on each id (graph order) and the initial queue.
+struct Schedule {
+    std::unordered_set<std::string> input_names;
+    std::vector<char> available;
+    std::vector<size_t> missing;
+    std::vector<std::vector<size_t>> waiting;
+    std::vector<size_t> queue;
+};
 
 class Interpreter {
 public:
@@ -30,9 +56,18 @@ public:
     TensorMap run(const TensorMap& inputs, InterpreterHook& hook, const RunOptions& opts) const;
 
 private:
+    std::shared_ptr<const Schedule> schedule_for(const TensorMap& inputs) const;
+
+    struct ScheduleCache {
+        std::mutex mu;
+        std::shared_ptr<const Schedule> last;
+    };
+
     Graph graph_;
     mutable std::unique_ptr<ConstCache> consts_;
     FusionPlan plan_;
+    BlockIndex index_;
+    mutable std::unique_ptr<ScheduleCache> sched_;
 };
 
 // Process-wide defaults for RunOptions (set through the C ABI or the

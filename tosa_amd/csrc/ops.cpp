@@ -29,8 +29,8 @@ TensorPtr ExecState::get(const std::string& name) const
 
 const TensorDef* ExecState::find_def(const std::string& name) const
 {
-    auto it = defs.find(name);
-    return it == defs.end() ? nullptr : it->second;
+    auto it = defs->find(name);
+    return it == defs->end() ? nullptr : it->second;
 }
 
 static Shape shape_from_ir(const std::vector<int32_t>& s)
@@ -60,8 +60,8 @@ TensorPtr ExecState::resolve(const std::string& name) const
     auto it = tensors.find(name);
     if (it != tensors.end())
         return it->second;
-    auto c = const_defs.find(name);
-    if (c == const_defs.end())
+    auto c = const_defs->find(name);
+    if (c == const_defs->end())
         return nullptr;
     try {
         auto t = std::make_shared<Tensor>();
@@ -798,8 +798,8 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         const void* x = input->data->device_in();
         const void* w = weight->data->device_in();
         // Weight and bias are graph constants: derived data may be cached.
-        const bool w_const = st.const_defs.count(op.inputs[1]) != 0;
-        const bool wb_const = w_const && st.const_defs.count(op.inputs[2]);
+        const bool w_const = st.is_const(op.inputs[1]);
+        const bool wb_const = w_const && st.is_const(op.inputs[2]);
         ConvI8Desc fd;
         bool fast = false;
         if (mfma_int || dw_int) {
@@ -839,7 +839,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
                                static_cast<int32_t*>(s->device_out()), st.s());
                 return s;
             };
-            wsum_keep = st.const_defs.count(op.inputs[1]) ? cached_aux(ws, AUX_WSUM, make) : make();
+            wsum_keep = st.is_const(op.inputs[1]) ? cached_aux(ws, AUX_WSUM, make) : make();
             wsum = static_cast<const int32_t*>(wsum_keep->device_in());
         }
         GemmDesc gd;
@@ -971,7 +971,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             const DType final_t = tail->rp.out_t;
             auto fin = new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], g.out_shape, final_t);
             const bool rs_const =
-                st.const_defs.count(tail->rop->inputs[1]) && st.const_defs.count(tail->rop->inputs[2]);
+                st.is_const(tail->rop->inputs[1]) && st.is_const(tail->rop->inputs[2]);
             if (count > 0)
                 launch(fin->data->device_out(), &tail->rp.rs, rs_const, st.err(), st.s());
             auto keep = tail->rp.params;
@@ -1067,7 +1067,7 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             if (wpb > 0) {
                 // Stride-1 convolution on the halo kernel, with its packed
                 // weights cached on a constant weight.
-                const bool w_const = st.const_defs.count(op.inputs[1]) != 0;
+                const bool w_const = st.is_const(op.inputs[1]);
                 const std::string key =
                     "conv_f16_wpack:" + std::to_string(wpb) + ":" + std::to_string(kern::conv_f16_halo_block(hd));
                 auto wp = derived_i8(*weight->data, key, wpb, w_const, st.s(),
@@ -1196,7 +1196,7 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
         // int8: the pointwise tiled kernel, one batch per grid slice, over B
         // transposed to rows of c bytes (cached when B is a graph constant);
         // zero points folded into the accumulator like CONV2D's.
-        const bool b_const = st.const_defs.count(op.inputs[1]) != 0;
+        const bool b_const = st.is_const(op.inputs[1]);
         ConvI8Desc fd;
         fd.x = static_cast<const int8_t*>(a_dev);
         fd.bias = nullptr;
@@ -1226,7 +1226,7 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
                 auto fin =
                     new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], out_shape, tail->rp.out_t);
                 const bool rs_const =
-                    st.const_defs.count(tail->rop->inputs[1]) && st.const_defs.count(tail->rop->inputs[2]);
+                    st.is_const(tail->rop->inputs[1]) && st.is_const(tail->rop->inputs[2]);
                 if (count > 0)
                     launch(fin->data->device_out(), &tail->rp.rs, rs_const, st.err(), st.s());
                 auto keep = tail->rp.params;
