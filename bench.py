@@ -42,8 +42,8 @@ METRIC = "int8 CONV2D+RESCALE TOPS (% MFMA peak); int8 MobileNetV2-style graph i
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=500)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--quick", action="store_true", help="headline workload only")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     p.add_argument("--only", default=None, help="run one workload (a WORKLOADS key) and print its timing")
