@@ -142,3 +142,41 @@ def test_options_round_trip():
     T.set_option("strict_float", old)
     with pytest.raises(T.TosaError):
         T.set_option("no_such_option", 1)
+
+
+def test_interpreter_replans_for_each_input_name_set():
+    # One Interpreter, runs alternating between complete and incomplete input
+    # sets: the ready queue's starting state is kept per set of input names,
+    # so each run must see its own set (tests/integration.rs:77-84 for the
+    # stuck case).
+    c = Case(os.path.join(ROOT, "tests", "golden", "networks", "tf_add_f32"))
+    interp = T.Interpreter.from_flatbuffer(c.graph)
+    for complete in (False, True, False, True):
+        ins = _tensors(c) if complete else _tensors(c)[1:]
+        if complete and T.device_count() > 0:
+            assert set(interp.run(ins)) == set(c.expected())
+            continue
+        with pytest.raises(T.TosaError) as e:
+            interp.run(ins)
+        if complete:  # the ADD became ready and reached the device check
+            assert e.value.kind == "Device", str(e.value)
+        else:
+            assert e.value.kind == "GraphError" and "stuck" in str(e.value)
+
+
+def test_identity_graph_reruns_with_other_input_names():
+    from tosa_amd.tosa_writer import GraphBuilder
+    g = GraphBuilder()
+    g.input("x", [2, 3], "INT8")
+    g.tensor("y", [2, 3], "INT8")
+    g.op("IDENTITY", ["x"], ["y"])
+    interp = T.Interpreter.from_flatbuffer(g.build(["y"]))
+    x = np.arange(6, dtype=np.int8).reshape(2, 3)
+    for name in ("x", "q", "x"):
+        if name == "x":
+            out = interp.run([T.Tensor.from_numpy("x", x, "INT8")])
+            assert np.array_equal(out["y"].numpy(), x)
+        else:
+            with pytest.raises(T.TosaError) as e:
+                interp.run([T.Tensor.from_numpy(name, x, "INT8")])
+            assert "stuck" in str(e.value)
