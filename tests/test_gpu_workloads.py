@@ -54,15 +54,22 @@ def test_cfg1_conv_rescale_full_size():
 
 @pytest.mark.parametrize("shape", [(64, 28, 28, 128, 128), (64, 14, 14, 256, 256)])
 def test_resnet_scale_conv_rescale(shape):
+    # Every image of the batch against the oracle (C loops, a few seconds).
     n, h, w, cin, cout = shape
     graph, ins, _ = W.conv_rescale(n=n, h=h, w=w, cin=cin, cout=cout)
     y = run(graph, ins)["y"].numpy()
-    x = ins["x"][0]
-    for img in (0, n - 1):
-        sub = {"x": (x[img:img + 1], "INT8")}
-        g1, _, _ = W.conv_rescale(n=1, h=h, w=w, cin=cin, cout=cout)
-        ref = oracle_run(g1, sub)["y"]
-        assert same_int(y[img], ref.vals), img
+    ref = oracle_run(graph, ins)["y"]
+    assert same_int(y, ref.vals)
+
+
+def _exact_matmul_i32(a, b, azp, bzp):
+    """sum_k (a - azp)(b - bzp) per batch through float64 GEMMs: every partial
+    sum is an integer below 2^53 (|terms| <= 255 * 255, K <= 2^20), so the
+    result is exact; then wrapped to int32 as the reference's AccI32."""
+    af = a.astype(np.float64) - azp
+    bf = b.astype(np.float64) - bzp
+    out = np.matmul(af, bf)
+    return ((out.astype(np.int64) + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int64)
 
 
 def test_cfg2_matmul_rescale():
@@ -71,20 +78,24 @@ def test_cfg2_matmul_rescale():
     yi = run(graph, ins, fusion=False)["y"].numpy()
     assert np.array_equal(y, yi)
     a, b = ins["a"][0], ins["b"][0]
-    for bi in (0, 7):
-        g1, _, _ = W.matmul_rescale(batch=1)
-        ref = oracle_run(g1, {"a": (a[bi:bi + 1], "INT8"), "b": (b[bi:bi + 1], "INT8")})["y"]
-        assert same_int(y[bi], ref.vals), bi
+    # Batch 0 through the oracle's own MATMUL + RESCALE.
+    g1, _, _ = W.matmul_rescale(batch=1)
+    ref0 = oracle_run(g1, {"a": (a[:1], "INT8"), "b": (b[:1], "INT8")})["y"]
+    assert same_int(y[0], ref0.vals)
+    # Every batch: exact accumulators, then the oracle's RESCALE.
+    acc = _exact_matmul_i32(a, b, -7, 2)
+    r = O.rescale(O.T("INT32", list(acc.shape), acc), O.T("INT32", [1], np.array([1518500250])),
+                  O.T("INT8", [1], np.array([38])), 0, 0, "INT8", True, 1, False, False, False)
+    assert same_int(y, r.vals)
+    # The exact accumulators agree with the oracle's on batch 0.
+    acc_ref = oracle_run(g1, {"a": (a[:1], "INT8"), "b": (b[:1], "INT8")}, outputs=["acc"])["acc"]
+    assert same_int(acc[0], acc_ref.vals)
 
 
 def test_cfg3_depthwise_and_avg_pool():
     graph, ins, _ = W.depthwise()
     y = run(graph, ins)["y"].numpy()
-    x = ins["x"][0]
-    for img in (0, 31):
-        g1, _, _ = W.depthwise(n=1)
-        ref = oracle_run(g1, {"x": (x[img:img + 1], "INT8")})["y"]
-        assert same_int(y[img], ref.vals), img
+    assert same_int(y, oracle_run(graph, ins)["y"].vals)  # all 32 images
     graph, ins, _ = W.avg_pool()
     assert same_int(run(graph, ins)["y"].numpy(), oracle_run(graph, ins)["y"].vals)
 
@@ -92,17 +103,33 @@ def test_cfg3_depthwise_and_avg_pool():
 def test_cfg4_mobilenet_v2_end_to_end():
     graph2, ins2, _ = W.mobilenet_v2(n=2)
     ref = oracle_run(graph2, ins2)["logits"]
+    ref2 = np.asarray(ref.vals).reshape(2, 1000)
     for fusion in (True, False):
         got = run(graph2, ins2, fusion)["logits"].numpy()
         assert same_int(got, ref.vals), fusion
-    # Full batch: images 0 and 1 of the 64-image input are the 2-image input
-    # (the same seeded stream), so their logits must be the same.
     graph64, ins64, _ = W.mobilenet_v2(n=64)
     x64 = ins64["input"][0]
+    # Images 0 and 1 of the 64-image input are the 2-image input (the same
+    # seeded stream), so their logits must be the same.
     assert np.array_equal(x64[:2], ins2["input"][0])
     got64 = run(graph64, ins64)["logits"].numpy()
     assert got64.shape == (1, 64, 1000)
     assert same_int(got64[0, :2], ref.vals)
+    # Every batch position: the two checked images tiled 32 times must give
+    # their oracle logits in all 64 rows.
+    tiled = np.ascontiguousarray(np.tile(ins2["input"][0], (32, 1, 1, 1)))
+    got_t = run(graph64, {"input": (tiled, "INT8")})["logits"].numpy().reshape(64, 1000)
+    for i in range(64):
+        assert same_int(got_t[i], ref2[i % 2]), i
+    # Every image of the real input: a batch in reversed order gives the
+    # reversed logits (each image lands on other tiles), and eight images
+    # spread over the batch match the oracle.
+    got_r = run(graph64, {"input": (np.ascontiguousarray(x64[::-1]), "INT8")})["logits"].numpy().reshape(64, 1000)
+    assert np.array_equal(got_r, got64.reshape(64, 1000)[::-1])
+    pick = [2, 9, 18, 27, 36, 45, 54, 63]
+    g8, _, _ = W.mobilenet_v2(n=8)
+    ref8 = oracle_run(g8, {"input": (np.ascontiguousarray(x64[pick]), "INT8")})["logits"]
+    assert same_int(got64.reshape(64, 1000)[pick], ref8.vals)
 
 
 def _torch_conv_ref(x_bits, w_bits, bias, dtype, pad):

@@ -58,6 +58,28 @@ size_t round_size(size_t b)
     return (b + g - 1) / g * g;
 }
 
+struct PinnedBlock {
+    void* p = nullptr;
+    size_t bytes = 0;
+    hipEvent_t ev = nullptr;  // recorded after the copy out of the block
+    bool held = false;        // acquired and not yet released
+};
+
+struct PinnedPool {
+    std::mutex mu;
+    std::vector<PinnedBlock> idle, busy;
+    size_t idle_bytes = 0;
+};
+
+PinnedPool& pinned_pool()
+{
+    static PinnedPool* p = new PinnedPool();  // never destroyed, like the device pools
+    return *p;
+}
+
+// Blocks kept for reuse beyond this many bytes go back to the driver.
+constexpr size_t PINNED_KEEP_BYTES = size_t(1) << 30;
+
 thread_local Stream* t_stream = nullptr;
 thread_local hipStream_t t_user_stream = nullptr;
 
@@ -153,6 +175,68 @@ void dev_free(void* p, size_t bytes, hipStream_t s)
     std::lock_guard<std::mutex> lk(P.mu);
     P.free[s].emplace(r, p);
     P.cached += r;
+}
+
+void* pinned_acquire(size_t bytes)
+{
+    const size_t r = round_size(bytes ? bytes : 1);
+    PinnedPool& P = pinned_pool();
+    {
+        std::lock_guard<std::mutex> lk(P.mu);
+        // Blocks whose copies have run become idle.
+        for (size_t i = 0; i < P.busy.size();) {
+            if (!P.busy[i].held && hipEventQuery(P.busy[i].ev) == hipSuccess) {
+                P.idle_bytes += P.busy[i].bytes;
+                P.idle.push_back(P.busy[i]);
+                P.busy[i] = P.busy.back();
+                P.busy.pop_back();
+            } else {
+                i++;
+            }
+        }
+        size_t best = P.idle.size();
+        for (size_t i = 0; i < P.idle.size(); i++)
+            if (P.idle[i].bytes >= r && (best == P.idle.size() || P.idle[i].bytes < P.idle[best].bytes))
+                best = i;
+        if (best < P.idle.size()) {
+            PinnedBlock b = P.idle[best];
+            P.idle[best] = P.idle.back();
+            P.idle.pop_back();
+            P.idle_bytes -= b.bytes;
+            b.held = true;  // the caller's until pinned_release
+            P.busy.push_back(b);
+            return b.p;
+        }
+        while (P.idle_bytes + r > PINNED_KEEP_BYTES && !P.idle.empty()) {
+            (void)hipHostFree(P.idle.back().p);
+            if (P.idle.back().ev)
+                (void)hipEventDestroy(P.idle.back().ev);
+            P.idle_bytes -= P.idle.back().bytes;
+            P.idle.pop_back();
+        }
+    }
+    PinnedBlock b;
+    hip_check(hipHostMalloc(&b.p, r, hipHostMallocDefault), "hipHostMalloc(staging)");
+    b.bytes = r;
+    b.held = true;
+    hip_check(hipEventCreateWithFlags(&b.ev, hipEventDisableTiming), "hipEventCreate(staging)");
+    std::lock_guard<std::mutex> lk(P.mu);
+    P.busy.push_back(b);
+    return b.p;
+}
+
+void pinned_release(void* p, hipStream_t s)
+{
+    PinnedPool& P = pinned_pool();
+    std::lock_guard<std::mutex> lk(P.mu);
+    for (auto& b : P.busy)
+        if (b.p == p && b.held) {
+            // The block stays busy until everything enqueued on `s` so far
+            // has run.
+            b.held = false;
+            hip_check(hipEventRecord(b.ev, s), "hipEventRecord(staging)");
+            return;
+        }
 }
 
 size_t dev_cached_bytes()

@@ -40,6 +40,12 @@ void* dev_alloc(size_t bytes, hipStream_t s);
 void dev_free(void* p, size_t bytes, hipStream_t s);
 size_t dev_cached_bytes();
 
+// Pinned host staging for uploads: pinned_acquire returns a page-locked
+// block of at least `bytes`; pinned_release hands it back once the work
+// enqueued on `s` so far (the copy out of it) has run, without waiting.
+void* pinned_acquire(size_t bytes);
+void pinned_release(void* p, hipStream_t s);
+
 // Reset / read the error word of a stream (read synchronises the stream).
 void clear_error_word(Stream& st);
 uint32_t read_error_word(Stream& st);

@@ -51,6 +51,7 @@ StoragePtr ConstCache::get(const TensorDef& def)
     const int64_t count = shape_count(shape_from_ir(def.shape));
     StoragePtr s = def.has_data ? storage_from_raw_bytes(def.dtype, def.data.data(), def.data.size(), count)
                                 : storage_zeros(def.dtype, count);
+    s->shared_const = true;
     map_[&def] = s;
     return s;
 }
@@ -198,23 +199,32 @@ std::pair<int64_t, int64_t> int_range(DType t)
     }
 }
 
-// Device copy of a host-computed array, cached on `owner` under `key`.
-StoragePtr cached_aux(Storage& owner, int kind, const std::function<StoragePtr()>& make)
-{
-    if (owner.aux && owner.aux_kind == kind)
-        return owner.aux;
-    owner.aux = make();
-    owner.aux_kind = kind;
-    return owner.aux;
-}
-
-enum AuxKind { AUX_WSUM = 1, AUX_F32 = 2, AUX_RESCALE = 3 };
-
 std::mutex& derived_mu()
 {
     static std::mutex mu;
     return mu;
 }
+
+// Data derived from a graph constant's storage by `make`, built once and
+// kept with it. Runs on several threads may share the constant: the slot is
+// read and filled under a lock (`make` runs outside it).
+StoragePtr cached_aux(Storage& owner, int kind, const std::function<StoragePtr()>& make)
+{
+    {
+        std::lock_guard<std::mutex> lk(derived_mu());
+        if (owner.aux && owner.aux_kind == kind)
+            return owner.aux;
+    }
+    StoragePtr made = make();
+    std::lock_guard<std::mutex> lk(derived_mu());
+    if (!(owner.aux && owner.aux_kind == kind)) {
+        owner.aux = made;
+        owner.aux_kind = kind;
+    }
+    return owner.aux;
+}
+
+enum AuxKind { AUX_WSUM = 1, AUX_F32 = 2 };
 
 // Epilogue table of the fast int8 convolution for `rs` (the plain int32
 // epilogue when null). Cached on the weight storage when everything it is
@@ -356,10 +366,21 @@ RescalePrep prepare_rescale(const ExecState& st, const Operator& op, const Tenso
     if (!zp_ok(in_t, izp, a.input_unsigned) || !zp_ok(out_t, ozp, a.output_unsigned))
         throw invalid(OP, "zero point not allowed for this type");
 
-    // Widened multiplier and shift, cached with the multiplier tensor (for
-    // CONST operands: once per graph). The key includes the shift storage.
+    // Multiplier and shift as int32 on the device. For graph constants they
+    // are built once per (multiplier, shift) pair and kept with the
+    // multiplier (never replaced, so their device address identifies them
+    // for as long as the graph lives); other operands are re-read and
+    // uploaded on every run, since their memory may change between runs.
+    const bool params_const = st.is_const(op.inputs[1]) && st.is_const(op.inputs[2]);
     Storage& ms = *multiplier->data;
-    const Storage* shift_key = shift->data.get();
+    char key[64];
+    std::snprintf(key, sizeof key, "rescale_params:%p", static_cast<const void*>(shift->data.get()));
+    if (params_const) {
+        std::lock_guard<std::mutex> lk(derived_mu());
+        auto it = ms.derived.find(key);
+        if (it != ms.derived.end())
+            p.params = it->second;
+    }
     std::vector<int64_t> mv = int_values(*multiplier), sv = int_values(*shift);
     if (shape_count(p.shape) > 0 && a.rounding_mode != ROUND_INEXACT) {
         for (int64_t c = 0; c < channels; c++) {
@@ -371,20 +392,20 @@ RescalePrep prepare_rescale(const ExecState& st, const Operator& op, const Tenso
                                            std::to_string(s));
         }
     }
-    if (!(ms.aux && ms.aux_kind == AUX_RESCALE && ms.aux->aux.get() == shift_key)) {
+    if (!p.params) {
         std::vector<int32_t> host(2 * channels);
         for (int64_t c = 0; c < channels; c++) {
             host[c] = int32_t(mv[c]);
             host[channels + c] = int32_t(sv[c]);
         }
-        auto params = make_host_storage(DT_INT32, 2 * channels, host.data());
-        // Remember which shift tensor these parameters were built from (a
-        // non-owning marker: the pointer is only compared).
-        params->aux = std::shared_ptr<Storage>(std::shared_ptr<Storage>(), const_cast<Storage*>(shift_key));
-        ms.aux = params;
-        ms.aux_kind = AUX_RESCALE;
+        p.params = make_host_storage(DT_INT32, 2 * channels, host.data());
+        if (params_const) {
+            p.params->shared_const = true;
+            std::lock_guard<std::mutex> lk(derived_mu());
+            auto ins = ms.derived.emplace(key, p.params);
+            p.params = ins.first->second;  // another run may have built it first
+        }
     }
-    p.params = ms.aux;
     const int32_t* dp = static_cast<const int32_t*>(p.params->device_in());
     RescaleDev& r = p.rs;
     r.mult = dp;
@@ -993,13 +1014,17 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
     }
 
     if (mfma_float && sizes_ok()) {
-        // Bias as f32 values, cached with the bias tensor.
+        // Bias as f32 values, kept with a constant bias tensor (rebuilt per
+        // run otherwise: the caller may rewrite a wrapped buffer).
         Storage& bs = *bias->data;
-        auto bf = cached_aux(bs, AUX_F32, [&]() {
+        auto make_bf = [&]() {
             std::vector<double> v = float_values(*bias);
             std::vector<float> f(v.begin(), v.end());
-            return make_host_storage(DT_FP32, int64_t(f.size()), f.data());
-        });
+            auto h = make_host_storage(DT_FP32, int64_t(f.size()), f.data());
+            h->shared_const = st.is_const(op.inputs[2]);
+            return h;
+        };
+        auto bf = st.is_const(op.inputs[2]) ? cached_aux(bs, AUX_F32, make_bf) : make_bf();
         GemmDesc gd;
         gd.is_conv = 1;
         gd.elem = in_t == DT_BF16 ? ELEM_BF16 : ELEM_F16;

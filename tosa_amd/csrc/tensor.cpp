@@ -9,6 +9,8 @@ namespace tosa {
 
 Storage::~Storage()
 {
+    if (ready)
+        (void)hipEventDestroy(ready);
     if (dev && !external)
         dev_free(dev, dev_bytes, dev_stream);
 }
@@ -23,19 +25,54 @@ static void ensure_alloc(Storage& s)
     s.dev = dev_alloc(s.dev_bytes, st.s);
 }
 
+// A stream other than the one that uploaded `s` waits for the upload.
+static void order_after_upload(Storage& s)
+{
+    if (!s.ready)
+        return;
+    Stream& st = thread_stream();
+    if (st.s != s.ready_stream)
+        hip_check(hipStreamWaitEvent(st.s, s.ready, 0), "hipStreamWaitEvent(upload)");
+}
+
 const void* Storage::device_in()
 {
-    if (dev_valid)
+    if (dev_valid.load(std::memory_order_acquire)) {
+        if (ready) {
+            std::lock_guard<std::recursive_mutex> lk(mu);
+            order_after_upload(*this);
+        }
         return dev;
+    }
+    std::lock_guard<std::recursive_mutex> lk(mu);
+    if (dev_valid.load(std::memory_order_acquire)) {
+        order_after_upload(*this);
+        return dev;
+    }
     if (host_valid) {
         ensure_alloc(*this);
         Stream& st = thread_stream();
-        if (bytes())
-            hip_check(hipMemcpyAsync(dev, host.data(), bytes(), hipMemcpyHostToDevice, st.s), "upload tensor");
-        // The host buffer must outlive the copy: synchronise before anyone
-        // may release or change it.
-        hip_check(hipStreamSynchronize(st.s), "hipStreamSynchronize(upload)");
-        dev_valid = true;
+        const size_t n = bytes();
+        if (shared_const) {
+            // A graph constant: any run, on any stream, may read it as soon as
+            // dev_valid is set, so the copy completes first (once per graph).
+            if (n)
+                hip_check(hipMemcpyAsync(dev, host.data(), n, hipMemcpyHostToDevice, st.s), "upload constant");
+            hip_check(hipStreamSynchronize(st.s), "hipStreamSynchronize(upload)");
+        } else if (n) {
+            // Through pinned staging: the copy is asynchronous for the host,
+            // and the staging block is reused only once the stream has passed
+            // the copy. Readers on other streams wait for `ready`.
+            void* stage = pinned_acquire(n);
+            std::memcpy(stage, host.data(), n);
+            hip_check(hipMemcpyAsync(dev, stage, n, hipMemcpyHostToDevice, st.s), "upload tensor");
+            pinned_release(stage, st.s);
+            if (!ready)
+                hip_check(hipEventCreateWithFlags(&ready, hipEventDisableTiming), "hipEventCreate(upload)");
+            hip_check(hipEventRecord(ready, st.s), "hipEventRecord(upload)");
+            ready_stream = st.s;
+        }
+        dev_valid.store(true, std::memory_order_release);
         return dev;
     }
     if (materialize) {
@@ -50,15 +87,19 @@ const void* Storage::device_in()
 
 void* Storage::device_out()
 {
+    std::lock_guard<std::recursive_mutex> lk(mu);
     ensure_alloc(*this);
-    dev_valid = true;
     host_valid = false;
+    dev_valid.store(true, std::memory_order_release);
     return dev;
 }
 
 const uint8_t* Storage::host_in()
 {
-    if (host_valid)
+    std::lock_guard<std::recursive_mutex> lk(mu);
+    // Caller-owned device memory may have been rewritten since the last read:
+    // its host mirror is never reused.
+    if (host_valid && !external)
         return host.data();
     device_in();
     host.resize(bytes());

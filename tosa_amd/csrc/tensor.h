@@ -19,9 +19,11 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <functional>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -36,11 +38,25 @@ struct Storage {
     void* dev = nullptr;
     size_t dev_bytes = 0;
     hipStream_t dev_stream = nullptr;  // allocator pool that owns `dev`
-    bool dev_valid = false;
-    bool external = false;  // `dev` belongs to the caller; never freed here
+    std::atomic<bool> dev_valid{false};
+    // `dev` belongs to the caller, who may rewrite it between runs: never
+    // freed here, and its host mirror is re-read on every host access.
+    bool external = false;
+    // A graph constant shared by every run (and thread) of an Interpreter:
+    // uploaded synchronously, so any stream may read it once dev_valid.
+    bool shared_const = false;
 
     std::vector<uint8_t> host;
-    bool host_valid = false;
+    std::atomic<bool> host_valid{false};
+
+    // Upload of the host mirror issued on `ready_stream` without waiting for
+    // it; another stream that reads `dev` first waits for `ready`.
+    hipEvent_t ready = nullptr;
+    hipStream_t ready_stream = nullptr;
+
+    // Guards the first-use transitions (allocation, upload, download,
+    // materialisation) of storages that several runs may share.
+    std::recursive_mutex mu;
 
     // An int8 convolution's epilogue table that rules out every failure of
     // apply_scale_32's range REQUIRE (set once the table is known on the
