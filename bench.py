@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     p.add_argument("--only", default=None, help="run one workload (a WORKLOADS key) and print its timing")
     p.add_argument("--copy-mib", type=int, default=0, help="with --only: also run device copies of this size")
+    p.add_argument("--option", action="append", default=[], metavar="KEY=VALUE",
+                   help="with --only: set a library option first (tosa_set_option, e.g. deferred=0)")
     return p.parse_args()
 
 
@@ -196,12 +198,18 @@ def run_only(args, torch, T, W, sleep):
     if args.only not in WORKLOADS:
         print(f"unknown workload {args.only!r}; choose one of {', '.join(WORKLOADS)}", file=sys.stderr)
         sys.exit(2)
+    for kv in args.option:
+        key, _, val = kv.partition("=")
+        T.set_option(key, int(val))
     builder, kw, unit_ops, _ = WORKLOADS[args.only]
     g, i, inf = getattr(W, builder)(**kw)
     r = Runner(T, torch, g, i)
     sec = r.wall(args.steps, args.warmup)
-    k = r.gpu_time(max(1, args.steps), sleep)
-    line = {"workload": args.only, "ms_per_step": sec * 1e3, "gpu_ms": k * 1e3, "GB_s": inf["bytes"] / k / 1e9}
+    # At most 50 runs queued behind the spin kernel: each holds its outputs
+    # until the events are read, and more would grow the device pool mid-way.
+    k = r.gpu_time(max(1, min(args.steps, 50)), sleep)
+    line = {"workload": args.only, "options": args.option, "ms_per_step": sec * 1e3, "gpu_ms": k * 1e3,
+            "GB_s": inf["bytes"] / k / 1e9}
     if unit_ops:
         line["TOPS"] = inf["ops"] / k / 1e12
     if args.copy_mib:
