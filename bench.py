@@ -109,8 +109,12 @@ class Runner:
         self.torch.cuda.synchronize()
 
     def wall(self, steps, warmup):
+        # The warm-up runs exactly as the timed ones do (each run's outputs
+        # held until the next run replaces them), so the device pool already
+        # holds the blocks the timed runs cycle through.
+        out = None
         for _ in range(warmup):
-            self.run()
+            out = self.run()
         self.sync()
         t0 = time.perf_counter()
         for _ in range(steps):

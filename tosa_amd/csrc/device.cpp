@@ -84,19 +84,32 @@ thread_local Stream* t_stream = nullptr;
 thread_local hipStream_t t_user_stream = nullptr;
 
 std::mutex g_err_mu;
-std::unordered_map<hipStream_t, uint32_t*> g_err_words;
+struct ErrWord {
+    uint32_t* dev = nullptr;
+    uint32_t* host = nullptr;
+};
+std::unordered_map<hipStream_t, ErrWord> g_err_words;
 
-uint32_t* error_word_for(hipStream_t s)
+// The device error word of stream `s` and the pinned host word it is read
+// back into (a copy into pageable memory takes the runtime's staged path,
+// about twice the round trip of one into pinned memory).
+ErrWord error_word_for(hipStream_t s)
 {
     std::lock_guard<std::mutex> lk(g_err_mu);
     auto it = g_err_words.find(s);
     if (it != g_err_words.end())
         return it->second;
+    ErrWord w;
     void* p = nullptr;
     hip_check(hipMalloc(&p, 256), "hipMalloc(error word)");
     hip_check(hipMemset(p, 0, 256), "hipMemset(error word)");
-    g_err_words[s] = static_cast<uint32_t*>(p);
-    return static_cast<uint32_t*>(p);
+    w.dev = static_cast<uint32_t*>(p);
+    void* h = nullptr;
+    hip_check(hipHostMalloc(&h, 64, hipHostMallocDefault), "hipHostMalloc(error word)");
+    w.host = static_cast<uint32_t*>(h);
+    *w.host = 0;
+    g_err_words[s] = w;
+    return w;
 }
 
 }  // namespace
@@ -117,7 +130,9 @@ Stream& thread_stream()
         static thread_local Stream user;
         if (user.s != t_user_stream) {
             user.s = t_user_stream;
-            user.err = error_word_for(t_user_stream);
+            const ErrWord w = error_word_for(t_user_stream);
+            user.err = w.dev;
+            user.err_host = w.host;
         }
         return user;
     }
@@ -126,7 +141,9 @@ Stream& thread_stream()
             throw Error(ERR_DEVICE, "no HIP device is available (the MI355X path needs a GPU)");
         Stream* st = new Stream();
         hip_check(hipStreamCreateWithFlags(&st->s, hipStreamNonBlocking), "hipStreamCreate");
-        st->err = error_word_for(st->s);
+        const ErrWord w = error_word_for(st->s);
+        st->err = w.dev;
+        st->err_host = w.host;
         t_stream = st;
     }
     return *t_stream;
@@ -250,10 +267,9 @@ void clear_error_word(Stream& st) { hip_check(hipMemsetAsync(st.err, 0, sizeof(u
 
 uint32_t read_error_word(Stream& st)
 {
-    uint32_t v = 0;
-    hip_check(hipMemcpyAsync(&v, st.err, sizeof(uint32_t), hipMemcpyDeviceToHost, st.s), "read error word");
+    hip_check(hipMemcpyAsync(st.err_host, st.err, sizeof(uint32_t), hipMemcpyDeviceToHost, st.s), "read error word");
     hip_check(hipStreamSynchronize(st.s), "hipStreamSynchronize");
-    return v;
+    return *static_cast<volatile uint32_t*>(st.err_host);
 }
 
 }  // namespace tosa

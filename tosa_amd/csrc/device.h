@@ -26,7 +26,8 @@ std::string device_error_message(uint32_t bits);
 
 struct Stream {
     hipStream_t s = nullptr;
-    uint32_t* err = nullptr;  // device error word of this stream
+    uint32_t* err = nullptr;       // device error word of this stream
+    uint32_t* err_host = nullptr;  // pinned host word it is read back into
 };
 
 // The calling thread's stream (created on first use), or the stream the
