@@ -9,8 +9,11 @@ output zp 5) at ResNet conv3_x scale, where int8 MFMA (not HBM) bounds it.
 
 The JSON line reports whole-job throughput (TOPS), the fused conv kernel's
 roofline (MFMA-bound; average duration from HIP events on the library's
-stream) and the CPU oracle timed on the host beside it; `extra` carries the
-other benchmark configurations (incl. the int8 MobileNetV2-style graph img/s).
+stream) and the CPU oracle timed on the host beside it (the calling thread
+pinned to one CPU for the CPU legs; the host's CPU count and model recorded);
+`extra` carries the other benchmark configurations, incl. the int8
+MobileNetV2-style graph img/s with its own CPU leg (the oracle's graph runner
+on a batch of 4, whose logits the GPU must match bit for bit).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
     python bench.py --only NAME [--copy-mib M]   # one workload, for profilers
@@ -152,6 +155,33 @@ def calibrate_sleep(torch, seconds):
     return int(min(seconds / per, 2 ** 31 - 1))
 
 
+def host_facts():
+    """The box's host CPU: logical CPUs, those this process may use, model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"host_cpus": os.cpu_count(), "host_cpus_allowed": len(os.sched_getaffinity(0)), "host_cpu_model": model}
+
+
+def pinned(fn):
+    """Run `fn` with the calling thread pinned to one CPU (the highest one it
+    may use), in-process; the previous mask is restored afterwards. Only this
+    thread moves: the GPU runtime's own threads keep their CPUs."""
+    before = os.sched_getaffinity(0)
+    core = max(before)
+    os.sched_setaffinity(0, {core})
+    try:
+        return fn(), core
+    finally:
+        os.sched_setaffinity(0, before)
+
+
 def cpu_baseline(seconds):
     """The oracle (C restatement of the reference loops, 1 thread) on a
     bounded sample of the headline workload: whole images of the batch until
@@ -177,6 +207,26 @@ def cpu_baseline(seconds):
             "sample": f"{done} of 64 images of the headline CONV2D+RESCALE ({done * info['macs']:.3g} MAC) "
                       f"through oracle/tosa_oracle.c (C restatement of the reference loops, 1 thread), "
                       f"{t_total:.1f} s"}, out0
+
+
+def cpu_mobilenet(n=4):
+    """The oracle's graph runner (C restatement of the reference's operators,
+    1 thread) on the int8 MobileNetV2-style graph at batch `n`: img/s, which
+    per image is the same figure as for the batch of 64, and the logits."""
+    from oracle import oracle as O
+    from oracle import tosa_reader as fb
+    from tosa_amd import workloads as W
+    g, ins, _ = W.mobilenet_v2(n=n)
+    blk = fb.main_block(g)
+    feeds = {k: O.T(dt, list(a.shape), O.decode(dt, a)) for k, (a, dt) in ins.items()}
+    t0 = time.perf_counter()
+    out = O.run_block(blk, feeds)
+    t = time.perf_counter() - t0
+    logits = out[blk.outputs[0]].vals
+    return {"img_s": n / t, "cores": 1, "kind": "port",
+            "sample": f"batch {n} of the same graph through the oracle's graph runner (oracle/oracle.py over "
+                      f"oracle/tosa_oracle.c, 1 thread), {t:.1f} s; img/s scales to the batch of 64 as is "
+                      f"(images are independent)"}, g, ins, logits
 
 
 def _conv_params():
@@ -265,7 +315,10 @@ def main():
     out_img0 = r.run()["y"].numpy()[0]
     r.sync()
 
-    cpu, cpu_img0 = cpu_baseline(args.cpu_seconds)
+    # CPU legs after every GPU figure of the headline, on one pinned core.
+    (cpu, cpu_img0), core = pinned(lambda: cpu_baseline(args.cpu_seconds))
+    cpu.update(host_facts())
+    cpu["pinned_cpu"] = core
     extra = {"headline_image0_bit_exact_vs_oracle": bool(np.array_equal(out_img0, cpu_img0[0])),
              "headline_kernel_us": kern * 1e6}
 
@@ -286,6 +339,14 @@ def main():
         inf, s, k = measure("mobilenet_v2_int8_n64")
         extra["mobilenet_v2_int8_n64"].update({"img_s": 64 / s, "img_s_gpu": 64 / k,
                                                "hbm_roofline_frac": inf["bytes"] / k / 1e9 / PEAK_HBM_GBS})
+        (mcpu, mg, mins, mlogits), core = pinned(cpu_mobilenet)
+        # The same batch-4 graph on the GPU, logits compared bit for bit.
+        got = Runner(T, torch, mg, mins).run()
+        name = next(iter(got))
+        mcpu["gpu_logits_bit_exact"] = bool(np.array_equal(got[name].numpy().reshape(-1).astype(np.int64),
+                                                           np.asarray(mlogits).reshape(-1).astype(np.int64)))
+        mcpu["pinned_cpu"] = core
+        extra["mobilenet_v2_int8_n64"]["cpu_baseline"] = mcpu
         for name in WORKLOADS:
             if name not in (HEADLINE, "mobilenet_v2_int8_n64"):
                 measure(name)
