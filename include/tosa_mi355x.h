@@ -177,6 +177,49 @@ tosa_status tosa_set_stream(void* hip_stream);
 tosa_status tosa_synchronize(void);
 int tosa_device_count(void);
 
+/* ---- op-level entry points (no graph) ----------------------------------------
+ * One operator on caller-owned device buffers, enqueued on `stream` (a
+ * hipStream_t; NULL: this thread's stream) and returning without waiting.
+ * They stand for the reference's per-operator boundary, ops::dispatch
+ * (src/ops/mod.rs:22), as conformance tests and benchmarks use it.
+ *
+ * A RESCALE of the int32 accumulator that follows the operator in a
+ * quantised graph: eval_rescale (src/ops/type_conv.rs:111-191) with
+ * scale32, input zero point 0 and apply_scale_32 (src/ops/quant.rs:17-32),
+ * then optionally CLAMP (src/ops/elementwise.rs:328-334). Host arrays. */
+typedef struct tosa_rescale_i32 {
+    const int32_t* multiplier; /* [channels], each >= 0 */
+    const int8_t* shift;       /* [channels], each in [2, 62] */
+    int32_t channels;          /* 1 (per tensor) or the output channels (per channel) */
+    int32_t double_round;      /* 1: DOUBLE_ROUND, 0: SINGLE_ROUND */
+    uint32_t output_dtype;     /* INT8, INT16 or INT32 (schema codes) */
+    int32_t output_zp;         /* an int8 value for INT8 output, 0 otherwise */
+    int32_t has_clamp;         /* 1: clamp the output values to [clamp_min, clamp_max] */
+    int32_t clamp_min, clamp_max;
+} tosa_rescale_i32;
+
+/* int8 CONV2D: eval_conv's integer branch (src/ops/conv.rs:398-474) with
+ * ConvNd::new's checks (src/ops/conv.rs:57-139). x NHWC [N,IH,IW,IC] and w
+ * OHWI [OC,KH,KW,IC] int8, bias int32 [1 or OC], all device pointers (x and
+ * w 16-byte aligned); pad {top, bottom, left, right}, stride {y, x},
+ * dilation {y, x}. out receives NHWC [N,OH,OW,OC]: int32 without
+ * `rescale`, else the rescale's output type; out_shape (may be NULL) the
+ * output shape; with out NULL the call only checks its arguments and fills
+ * out_shape. A value that fails apply_scale_32's range REQUIRE sets bits
+ * in *device_error (a device word the caller clears and reads); with
+ * device_error NULL, in the error word of this thread's stream, which the
+ * next tosa_synchronize reports (then `stream` must be NULL or this thread's
+ * stream). Derived data (epilogue table, packed weights) is rebuilt on every
+ * call in workspace from the stream's pool. Input channels must be a
+ * multiple of 16 for an unpadded 1x1 stride-1 convolution and of 64 for any
+ * other (TOSA_ERR_UNSUPPORTED_OP otherwise: run such a convolution through
+ * a graph). */
+tosa_status tosa_conv2d_i8(const int8_t* x, const int64_t x_shape[4], const int8_t* w, const int64_t w_shape[4],
+                           const int32_t* bias, int64_t bias_len, int32_t input_zp, int32_t weight_zp,
+                           const int32_t pad[4], const int32_t stride[2], const int32_t dilation[2],
+                           const tosa_rescale_i32* rescale, void* out, int64_t out_shape[4],
+                           uint32_t* device_error, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,20 @@ class HookCallbacks(ctypes.Structure):
     ]
 
 
+class RescaleI32(ctypes.Structure):
+    """tosa_rescale_i32 (include/tosa_mi355x.h)."""
+    _fields_ = [
+        ("multiplier", P), ("shift", P), ("channels", ctypes.c_int32), ("double_round", ctypes.c_int32),
+        ("output_dtype", ctypes.c_uint32), ("output_zp", ctypes.c_int32), ("has_clamp", ctypes.c_int32),
+        ("clamp_min", ctypes.c_int32), ("clamp_max", ctypes.c_int32),
+    ]
+
+
+_I64P = ctypes.POINTER(ctypes.c_int64)
+_I32P = ctypes.POINTER(ctypes.c_int32)
+_CONV2D_I8_ARGS = [P, _I64P, P, _I64P, P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _I32P, _I32P, _I32P,
+                   ctypes.POINTER(RescaleI32), P, _I64P, P, P]
+
 # name -> (restype, argtypes); every function declared in include/tosa_mi355x.h
 SIGNATURES = {
     "tosa_last_error": (ctypes.c_char_p, []),
@@ -125,6 +139,7 @@ SIGNATURES = {
     "tosa_set_stream": (ctypes.c_int, [P]),
     "tosa_synchronize": (ctypes.c_int, []),
     "tosa_device_count": (ctypes.c_int, []),
+    "tosa_conv2d_i8": (ctypes.c_int, _CONV2D_I8_ARGS),
 }
 
 

@@ -263,6 +263,8 @@ size_t dev_cached_bytes()
     return P.cached;
 }
 
+uint32_t* stream_error_word(hipStream_t s) { return error_word_for(s).dev; }
+
 void clear_error_word(Stream& st) { hip_check(hipMemsetAsync(st.err, 0, sizeof(uint32_t), st.s), "clear error word"); }
 
 uint32_t read_error_word(Stream& st)

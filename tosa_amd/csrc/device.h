@@ -50,6 +50,9 @@ void pinned_release(void* p, hipStream_t s);
 // Reset / read the error word of a stream (read synchronises the stream).
 void clear_error_word(Stream& st);
 uint32_t read_error_word(Stream& st);
+// The device error word of stream `s` (created on first use; the one that
+// thread_stream() carries when `s` is the thread's stream).
+uint32_t* stream_error_word(hipStream_t s);
 
 int device_count();
 bool device_available();
