@@ -138,6 +138,7 @@ def test_conv2d_i8_range_require_reported():
     bt, bp = dev(bias)
     out = torch.empty(1 * 6 * 28 * 32, dtype=torch.uint8, device="cuda")
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()  # the zero fill ran on torch's stream, the call runs on the library's
     T.conv2d_i8(xp, x.shape, wp, w.shape, bp, 32, 0, 0, (1, 1, 1, 1), (1, 1), (1, 1), rescale, out.data_ptr(),
                 err.data_ptr())
     T.synchronize()
