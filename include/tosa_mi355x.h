@@ -220,6 +220,23 @@ tosa_status tosa_conv2d_i8(const int8_t* x, const int64_t x_shape[4], const int8
                            const tosa_rescale_i32* rescale, void* out, int64_t out_shape[4],
                            uint32_t* device_error, void* stream);
 
+/* No counterpart in the reference: tosa_conv2d_i8 for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results, but the
+ * epilogue table, packed weights and RESCALE words live in a static array of
+ * 4 MiB per GPU (held until the process ends) instead of pool memory: no
+ * hipMalloc, hipFree or host staging, and the RESCALE words are written by a
+ * kernel from its own arguments. A call whose workspace exceeds the array is
+ * rejected (TOSA_ERR_INVALID_ARGUMENT), as is a call with a RESCALE and no
+ * device_error. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams or threads) race. `stream` NULL is HIP's
+ * null stream. */
+tosa_status tosa_conv2d_i8_noalloc(const int8_t* x, const int64_t x_shape[4], const int8_t* w,
+                                   const int64_t w_shape[4], const int32_t* bias, int64_t bias_len, int32_t input_zp,
+                                   int32_t weight_zp, const int32_t pad[4], const int32_t stride[2],
+                                   const int32_t dilation[2], const tosa_rescale_i32* rescale, void* out,
+                                   int64_t out_shape[4], uint32_t* device_error, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

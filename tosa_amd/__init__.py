@@ -401,7 +401,7 @@ def set_stream(stream_ptr: int | None):
 
 
 def conv2d_i8(x_ptr, x_shape, w_ptr, w_shape, bias_ptr, bias_len, input_zp=0, weight_zp=0, pad=(0, 0, 0, 0),
-              stride=(1, 1), dilation=(1, 1), rescale=None, out_ptr=0, device_error=0, stream=0):
+              stride=(1, 1), dilation=(1, 1), rescale=None, out_ptr=0, device_error=0, stream=0, no_alloc=False):
     """Op-level int8 CONV2D on device buffers (tosa_conv2d_i8): x NHWC and w
     OHWI int8, bias int32, out NHWC (int32, or the rescale's type), given as
     device addresses; returns the output shape. `rescale` is None or a dict
@@ -409,7 +409,8 @@ def conv2d_i8(x_ptr, x_shape, w_ptr, w_shape, bias_ptr, bias_len, input_zp=0, we
     output_dtype ("INT8"/"INT16"/"INT32"), output_zp and optional clamp
     (lo, hi). Enqueued on `stream` (0: this thread's stream); REQUIRE
     failures go to the device word at `device_error` (0: the stream's own,
-    reported by synchronize())."""
+    reported by synchronize()). `no_alloc`: tosa_conv2d_i8_noalloc (workspace in
+    the per-GPU static array; `stream` 0 is then HIP's null stream)."""
     xs = (ctypes.c_int64 * 4)(*x_shape)
     ws = (ctypes.c_int64 * 4)(*w_shape)
     pd = (ctypes.c_int32 * 4)(*pad)
@@ -426,10 +427,10 @@ def conv2d_i8(x_ptr, x_shape, w_ptr, w_shape, bias_ptr, bias_len, input_zp=0, we
                              DTYPE_CODE[rescale.get("output_dtype", "INT8")], int(rescale.get("output_zp", 0)),
                              int(clamp is not None), int(clamp[0]) if clamp else 0, int(clamp[1]) if clamp else 0)
         rs_p = ctypes.pointer(rs)
-    check(lib().tosa_conv2d_i8(ctypes.c_void_p(x_ptr), xs, ctypes.c_void_p(w_ptr), ws, ctypes.c_void_p(bias_ptr),
-                               int(bias_len), int(input_zp), int(weight_zp), pd, st, dl, rs_p,
-                               ctypes.c_void_p(out_ptr), os_, ctypes.c_void_p(device_error or 0),
-                               ctypes.c_void_p(stream or 0)))
+    fn = lib().tosa_conv2d_i8_noalloc if no_alloc else lib().tosa_conv2d_i8
+    check(fn(ctypes.c_void_p(x_ptr), xs, ctypes.c_void_p(w_ptr), ws, ctypes.c_void_p(bias_ptr), int(bias_len),
+             int(input_zp), int(weight_zp), pd, st, dl, rs_p, ctypes.c_void_p(out_ptr), os_,
+             ctypes.c_void_p(device_error or 0), ctypes.c_void_p(stream or 0)))
     del keep
     return tuple(os_)
 

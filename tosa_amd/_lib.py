@@ -140,6 +140,7 @@ SIGNATURES = {
     "tosa_synchronize": (ctypes.c_int, []),
     "tosa_device_count": (ctypes.c_int, []),
     "tosa_conv2d_i8": (ctypes.c_int, _CONV2D_I8_ARGS),
+    "tosa_conv2d_i8_noalloc": (ctypes.c_int, _CONV2D_I8_ARGS),
 }
 
 

@@ -624,4 +624,31 @@ tosa_status tosa_conv2d_i8(const int8_t* x, const int64_t x_shape[4], const int8
     });
 }
 
+tosa_status tosa_conv2d_i8_noalloc(const int8_t* x, const int64_t x_shape[4], const int8_t* w,
+                                   const int64_t w_shape[4], const int32_t* bias, int64_t bias_len, int32_t input_zp,
+                                   int32_t weight_zp, const int32_t pad[4], const int32_t stride[2],
+                                   const int32_t dilation[2], const tosa_rescale_i32* rescale, void* out,
+                                   int64_t out_shape[4], uint32_t* device_error, void* stream)
+{
+    return guard([&] {
+        ConvI8Args a;
+        a.x = x;
+        a.x_shape = x_shape;
+        a.w = w;
+        a.w_shape = w_shape;
+        a.bias = bias;
+        a.bias_len = bias_len;
+        a.input_zp = input_zp;
+        a.weight_zp = weight_zp;
+        a.pad = pad;
+        a.stride = stride;
+        a.dilation = dilation;
+        a.rescale = rescale;
+        a.out = out;
+        a.device_error = device_error;
+        a.stream = stream;
+        conv2d_i8_noalloc(a, out_shape);
+    });
+}
+
 }  // extern "C"

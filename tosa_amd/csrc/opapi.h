@@ -55,5 +55,7 @@ ConvI8Call prepare_conv2d_i8(const ConvI8Args& a);
 void launch_conv2d_i8(const ConvI8Call& c, uint8_t* ws, void* out, uint32_t* err, hipStream_t s);
 // tosa_conv2d_i8: workspace from the stream's pool.
 void conv2d_i8(const ConvI8Args& a, int64_t* out_shape);
+// tosa_conv2d_i8_noalloc: workspace in the per-GPU static scratch array.
+void conv2d_i8_noalloc(const ConvI8Args& a, int64_t* out_shape);
 
 }  // namespace tosa

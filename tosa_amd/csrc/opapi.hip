@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -44,6 +45,65 @@ int64_t extent(int64_t in, int32_t pb, int32_t pa, int64_t k, int32_t d, int32_t
 }
 
 int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Workspace of tosa_conv2d_i8_noalloc: one array per GPU, for the life of
+// the process. Its first 256 bytes are a discard error word (written by no
+// kernel in the calls that use it: those without a RESCALE); the rest holds
+// one call's workspace. Host code never passes the array's name to a kernel
+// (on the host it is a stand-in, not a device address): it uses the address
+// hipGetSymbolAddress reports for the current device.
+constexpr size_t SCRATCH_BYTES = size_t(4) << 20;
+constexpr size_t SCRATCH_WORKSPACE = SCRATCH_BYTES - 256;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (each GPU holds its own copy at its own address).
+uint8_t* scratch_on_current_device()
+{
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= MAX_DEVICES)
+        throw Error(ERR_DEVICE, "device index " + std::to_string(dev) + " beyond the scratch table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            throw Error(ERR_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+// RESCALE multiplier/shift words written into device memory from the
+// kernel's own arguments (no staging buffer, nothing a graph capture could
+// not record).
+constexpr int PARAM_WORDS = 240;
+struct ParamWords {
+    int32_t v[PARAM_WORDS];
+    int32_t n;
+};
+
+__global__ void __launch_bounds__(256) put_param_words(int32_t* dst, ParamWords p)
+{
+    const int i = int(threadIdx.x);
+    if (i < p.n)
+        dst[i] = p.v[i];
+}
+
+void upload_words(const std::vector<int32_t>& words, int32_t* dst, hipStream_t s)
+{
+    for (size_t i0 = 0; i0 < words.size(); i0 += PARAM_WORDS) {
+        ParamWords p{};
+        p.n = int32_t(std::min<size_t>(PARAM_WORDS, words.size() - i0));
+        std::memcpy(p.v, words.data() + i0, size_t(p.n) * sizeof(int32_t));
+        hipLaunchKernelGGL(put_param_words, dim3(1), dim3(256), 0, s, dst + i0, p);
+    }
+}
 
 }  // namespace
 
@@ -237,6 +297,28 @@ void conv2d_i8(const ConvI8Args& a, int64_t* out_shape)
     }
     launch_conv2d_i8(c, ws, a.out, err, s);
     dev_free(ws, size_t(c.workspace), s);
+}
+
+void conv2d_i8_noalloc(const ConvI8Args& a, int64_t* out_shape)
+{
+    const ConvI8Call c = prepare_conv2d_i8(a);
+    if (out_shape)
+        std::memcpy(out_shape, c.out_shape, sizeof c.out_shape);
+    if (size_t(c.workspace) > SCRATCH_WORKSPACE)
+        throw bad_arg(std::string(OP) + ": needs " + std::to_string(c.workspace) +
+                      " bytes of workspace; tosa_conv2d_i8_noalloc holds at most " +
+                      std::to_string(SCRATCH_WORKSPACE) + " (use tosa_conv2d_i8)");
+    if (c.has_rs && !a.device_error)
+        throw bad_arg(std::string(OP) + ": tosa_conv2d_i8_noalloc needs device_error with a RESCALE");
+    if (c.count == 0 || !a.out)
+        return;
+    uint8_t* base = scratch_on_current_device();
+    const hipStream_t s = static_cast<hipStream_t>(a.stream);  // NULL: HIP's null stream
+    uint32_t* err = a.device_error ? a.device_error : reinterpret_cast<uint32_t*>(base);
+    uint8_t* ws = base + 256;
+    if (!c.params.empty())
+        upload_words(c.params, reinterpret_cast<int32_t*>(ws + c.params_off), s);
+    launch_conv2d_i8(c, ws, a.out, err, s);
 }
 
 }  // namespace tosa
