@@ -8,8 +8,9 @@ TEST INFRASTRUCTURE ONLY. Imported by `tests/`, `__graft_entry__.smoke()` and
 interpreter does (src/interpreter.rs:154-245): a ready queue seeded in
 operator order, CONST always ready, a full rescan after each operator. Each
 operator's arithmetic is delegated to the C restatement; CLAMP, ADD,
-RESHAPE, TRANSPOSE, CONST and IDENTITY, which are plain data movement or one
-integer/float operation per element, are restated here with numpy.
+RESHAPE, TRANSPOSE, CONST, IDENTITY, MAX_POOL2D and CAST, which are plain
+data movement, a window maximum or one integer/float operation per element,
+are restated here with numpy (MATMUL_T as MATMUL on B rearranged).
 
 Values are held widened, as the reference does: every integer type as int64,
 every float type as float32 holding a value exactly representable in its
@@ -75,6 +76,11 @@ def lib():
         L.orc_avg_pool_int.argtypes = [P] + [ctypes.c_int] * 4 + [P, P, P, i64, i64, i64, i64, P]
         L.orc_avg_pool_float.argtypes = [P] + [ctypes.c_int] * 4 + [P, P, P, ctypes.c_int, P]
         L.orc_rescale.argtypes = [P, i64, P, P, i64] + [ctypes.c_int] * 7 + [i64, i64, P]
+        L.orc_conv3d.argtypes = [ctypes.c_int] + [P] * 6 + [ctypes.c_int] * 10 + [P, P, P, i64, i64, ctypes.c_int,
+                                                                                 ctypes.c_int, P, P]
+        L.orc_transpose_conv2d.argtypes = [ctypes.c_int] + [P] * 6 + [ctypes.c_int] * 8 + [P, P, i64, i64,
+                                                                                         ctypes.c_int, ctypes.c_int,
+                                                                                         P, P]
         L.orc_encode_array.argtypes = [ctypes.c_int, P, i64, P]
         L.orc_decode_array.argtypes = [ctypes.c_int, P, i64, P]
         L.orc_round_array.argtypes = [ctypes.c_int, P, i64, P]
@@ -203,6 +209,141 @@ def matmul(a: T, b: T, a_zp, b_zp, out_t) -> T:
         out = np.empty(n * h * w, dtype=np.float32)
         L.orc_matmul_float(_p(av), _p(bv), n, h, c, w, MM_FACC[out_t], _p(out))
     return T(out_t, [n, h, w], out)
+
+
+def _conv_operands(x: T, w: T, bias: T, acc_type):
+    """Operand arrays of the C convolutions: the integer branch takes int64
+    values, the float one float32 (the accumulator kind and output format
+    come from acc_type and the bias type, src/ops/conv.rs:475-496)."""
+    if acc_type in ("INT32", "INT48"):
+        cast = lambda t: np.ascontiguousarray(t.vals, dtype=np.int64)  # noqa: E731
+        return 1, (cast(x), cast(w), cast(bias), None, None, None), 0 if acc_type == "INT32" else 1, 0
+    cast = lambda t: np.ascontiguousarray(t.vals, dtype=np.float32)  # noqa: E731
+    return 0, (None, None, None, cast(x), cast(w), cast(bias)), FACC[acc_type], FMT[bias.dtype]
+
+
+def conv3d(x: T, w: T, bias: T, in_zp, w_zp, pad, stride, dilation, acc_type) -> T:
+    """CONV3D: src/ops/conv.rs:505-511 (ConvNd with three spatial dimensions,
+    :92-181) through eval_conv (:398-500)."""
+    L = lib()
+    n, id_, ih, iw, ic = x.shape
+    oc, kd, kh, kw, _ = w.shape
+    ext = lambda i, a, b, k, d, s: (i - 1 + a + b - (k - 1) * d) // s + 1  # noqa: E731
+    od = ext(id_, pad[0], pad[1], kd, dilation[0], stride[0])
+    oh = ext(ih, pad[2], pad[3], kh, dilation[1], stride[1])
+    ow = ext(iw, pad[4], pad[5], kw, dilation[2], stride[2])
+    is_int, ops_, kind, fmt = _conv_operands(x, w, bias, acc_type)
+    count = n * od * oh * ow * oc
+    out_i = np.empty(count, dtype=np.int64) if is_int else None
+    out_f = None if is_int else np.empty(count, dtype=np.float32)
+    arr = lambda v, t: np.ascontiguousarray(v, dtype=t)  # noqa: E731
+    pd, st, dl = arr(pad, np.int32), arr(stride, np.int32), arr(dilation, np.int32)
+    L.orc_conv3d(is_int, *[_p(a) if a is not None else None for a in ops_], len(bias.vals), n, id_, ih, iw, ic, oc,
+                 kd, kh, kw, _p(pd), _p(st), _p(dl), int(in_zp) if is_int else 0, int(w_zp) if is_int else 0, kind,
+                 fmt, _p(out_i) if is_int else None, None if is_int else _p(out_f))
+    return T(bias.dtype, [n, od, oh, ow, oc], out_i if is_int else out_f)
+
+
+def transpose_conv2d(x: T, w: T, bias: T, in_zp, w_zp, out_pad, stride, acc_type) -> T:
+    """TRANSPOSE_CONV2D: src/ops/conv.rs:526-532 (Transpose, :268-372) through
+    eval_conv (:398-500)."""
+    L = lib()
+    n, ih, iw, ic = x.shape
+    oc, kh, kw, _ = w.shape
+    oh = (ih - 1) * stride[0] + out_pad[0] + out_pad[1] + kh
+    ow = (iw - 1) * stride[1] + out_pad[2] + out_pad[3] + kw
+    is_int, ops_, kind, fmt = _conv_operands(x, w, bias, acc_type)
+    count = n * oh * ow * oc
+    out_i = np.empty(count, dtype=np.int64) if is_int else None
+    out_f = None if is_int else np.empty(count, dtype=np.float32)
+    op_ = np.ascontiguousarray(out_pad, dtype=np.int32)
+    st = np.ascontiguousarray(stride, dtype=np.int32)
+    L.orc_transpose_conv2d(is_int, *[_p(a) if a is not None else None for a in ops_], len(bias.vals), n, ih, iw, ic,
+                           oc, kh, kw, _p(op_), _p(st), int(in_zp) if is_int else 0, int(w_zp) if is_int else 0,
+                           kind, fmt, _p(out_i) if is_int else None, None if is_int else _p(out_f))
+    return T(bias.dtype, [n, oh, ow, oc], out_i if is_int else out_f)
+
+
+def matmul_t(a: T, b: T, a_zp, b_zp, out_t) -> T:
+    """MATMUL_T: src/ops/matmul.rs:180-182, eval (:98-174) with b [D,W,C], D = N
+    or 1 (broadcast, Dims::b_index :74-77): MATMUL on b laid out [N,C,W]."""
+    bt = b.array().transpose(0, 2, 1)
+    if bt.shape[0] != a.shape[0]:
+        bt = np.broadcast_to(bt, (a.shape[0],) + bt.shape[1:])
+    return matmul(a, T(b.dtype, list(bt.shape), np.ascontiguousarray(bt).reshape(-1)), a_zp, b_zp, out_t)
+
+
+def max_pool2d(x: T, kernel, stride, pad, nan_mode) -> T:
+    """MAX_POOL2D: src/ops/pool.rs:233-286; windows as for_each_window
+    (:77-104, padding positions skipped, (ky, kx) order); integers fold
+    i64::max from the type's minimum, floats nan_max (common.rs:155-177:
+    ties keep the running value) from the type's lowest value, or from NaN
+    under IGNORE."""
+    n, ih, iw, c = x.shape
+    oh = (ih + pad[0] + pad[1] - kernel[0]) // stride[0] + 1
+    ow = (iw + pad[2] + pad[3] - kernel[1]) // stride[1] + 1
+    xa = x.array()
+    oy = np.arange(oh) * stride[0] - pad[0]
+    ox = np.arange(ow) * stride[1] - pad[2]
+    is_int = x.dtype in INT_TYPES
+    ignore = nan_mode == 2
+    if is_int:
+        m = np.full((n, oh, ow, c), INT_RANGE[x.dtype][0], dtype=np.int64)
+    else:
+        init = np.float32(np.nan) if ignore else np.float32(-448.0 if x.dtype == "FP8E4M3" else -np.inf)
+        m = np.full((n, oh, ow, c), init, dtype=np.float32)
+    for ky in range(kernel[0]):
+        y = oy + ky
+        vy = (y >= 0) & (y < ih)
+        for kx in range(kernel[1]):
+            xx = ox + kx
+            vx = (xx >= 0) & (xx < iw)
+            valid = (vy[:, None] & vx[None, :])[None, :, :, None]
+            v = xa[:, np.clip(y, 0, ih - 1)][:, :, np.clip(xx, 0, iw - 1)]
+            if is_int:
+                nm = np.maximum(m, v)
+            else:
+                with np.errstate(invalid="ignore"):
+                    either = np.isnan(m) | np.isnan(v)
+                    picked = np.where(np.isnan(m), v, m) if ignore else np.float32(np.nan)
+                    nm = np.where(either, picked, np.where(m >= v, m, v)).astype(np.float32)
+            m = np.where(valid, nm, m)
+    out = m.reshape(-1)
+    return T(x.dtype, [n, oh, ow, c], out if is_int else round_to(x.dtype, out))
+
+
+def _wrap(dtype, v):
+    """int_data's truncation to an integer type (src/ops/common.rs:110-122)."""
+    bits = {"INT8": 8, "INT16": 16, "INT32": 32}.get(dtype)
+    v = v.astype(np.int64)
+    if bits is None:
+        return v
+    return ((v + (1 << (bits - 1))) & ((1 << bits) - 1)) - (1 << (bits - 1))
+
+
+def cast(x: T, to) -> T:
+    """CAST: src/ops/type_conv.rs:45-80 (float_to_int :34-43: saturation
+    bounds taken in the input's precision, otherwise round half to even;
+    integers reach floats through FP32; int to int wraps)."""
+    frm, v = x.dtype, x.vals
+    if frm == "BOOL":
+        out = v.astype(np.float32) if to == "FP32" else _wrap(to, v.astype(np.int64))
+    elif to == "BOOL":
+        out = v != 0
+    elif frm in INT_TYPES:
+        out = _wrap(to, v) if to in INT_TYPES else round_to(to, v.astype(np.int64).astype(np.float32))
+    elif to in INT_TYPES:
+        lo, hi = INT_RANGE.get(to, (-(2 ** 63), 2 ** 63 - 1))
+        f = v.astype(np.float32)
+        hi_r = round_to(frm, np.array([hi], dtype=np.float32))[0]
+        lo_r = round_to(frm, np.array([lo], dtype=np.float32))[0]
+        with np.errstate(invalid="ignore"):
+            r = np.where(np.isnan(f), 0.0, np.rint(f)).astype(np.float64)
+            out = np.where(f >= hi_r, hi, np.where(f <= lo_r, lo, r)).astype(np.int64)
+        out = _wrap(to, out)
+    else:
+        out = round_to(to, v.astype(np.float32))
+    return T(to, x.shape, out)
 
 
 def avg_pool2d(x: T, in_zp, out_zp, kernel, stride, pad, acc_type) -> T:
@@ -335,6 +476,21 @@ def _eval(o, tensors, defs):
     elif o.op == "MATMUL":
         out_t = decl.dtype if decl else {"INT8": "INT32", "INT16": "INT48", "FP16": "FP16"}.get(g[0].dtype, "FP32")
         r = matmul(g[0], g[1], _single(g[2]), _single(g[3]), out_t)
+    elif o.op == "CONV3D":
+        r = conv3d(g[0], g[1], g[2], _single(g[3]), _single(g[4]), a["pad"], a["stride"], a["dilation"],
+                   fb.DTYPE_NAMES[a["acc_type"]])
+    elif o.op == "TRANSPOSE_CONV2D":
+        r = transpose_conv2d(g[0], g[1], g[2], _single(g[3]), _single(g[4]), a["out_pad"], a["stride"],
+                             fb.DTYPE_NAMES[a["acc_type"]])
+    elif o.op == "MATMUL_T":
+        # default_output (src/ops/matmul.rs:53-61)
+        dflt = {"INT8": "INT32", "INT16": "INT48", "FP16": "FP16", "FP8E4M3": "FP16", "FP8E5M2": "FP16"}
+        out_t = decl.dtype if decl else dflt.get(g[0].dtype, "FP32")
+        r = matmul_t(g[0], g[1], _single(g[2]), _single(g[3]), out_t)
+    elif o.op == "MAX_POOL2D":
+        r = max_pool2d(g[0], a["kernel"], a["stride"], a["pad"], a["nan_mode"])
+    elif o.op == "CAST":
+        r = cast(g[0], decl.dtype)
     elif o.op == "AVG_POOL2D":
         r = avg_pool2d(g[0], _single(g[1]), _single(g[2]), a["kernel"], a["stride"], a["pad"],
                        fb.DTYPE_NAMES[a["acc_type"]])

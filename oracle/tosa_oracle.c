@@ -434,6 +434,126 @@ void orc_matmul_float(const float *a, const float *b, int n, int h, int c, int w
             }
 }
 
+/* CONV3D: ConvNd::accumulate with three spatial dimensions
+ * (src/ops/conv.rs:149-181: batch, output position (d, y, x), oc, then the
+ * kernel position row-major (kd, ky, kx) and ic innermost), eval_conv's
+ * epilogue (:457-496). x [N,ID,IH,IW,IC], w [OC,KD,KH,KW,IC]; pad
+ * {front, back, top, bottom, left, right}, stride/dil {d, y, x}. `is_int`
+ * selects the integer branch (xi/wi/bi, acc_kind ACC_I32/ACC_I48) or the
+ * float one (xf/wf/bf, acc_kind FACC_*, out_fmt). */
+void orc_conv3d(int is_int, const int64_t *xi, const int64_t *wi, const int64_t *bi, const float *xf, const float *wf,
+                const float *bf, int bias_len, int n, int id, int ih, int iw, int ic, int oc, int kd, int kh, int kw,
+                const int32_t *pad, const int32_t *stride, const int32_t *dil, int64_t in_zp, int64_t w_zp,
+                int acc_kind, int out_fmt, int64_t *out_i, float *out_f)
+{
+    int od = conv_extent(id, pad[0], pad[1], kd, dil[0], stride[0]);
+    int oh = conv_extent(ih, pad[2], pad[3], kh, dil[1], stride[1]);
+    int ow = conv_extent(iw, pad[4], pad[5], kw, dil[2], stride[2]);
+    int64_t o = 0;
+    for (int b = 0; b < n; b++)
+        for (int oz = 0; oz < od; oz++)
+            for (int oy = 0; oy < oh; oy++)
+                for (int ox = 0; ox < ow; ox++)
+                    for (int co = 0; co < oc; co++) {
+                        uint32_t acc32 = 0;
+                        uint64_t acc64 = 0;
+                        float accf = 0.0f;
+                        for (int kz = 0; kz < kd; kz++) {
+                            int z = oz * stride[0] + kz * dil[0] - pad[0];
+                            if (z < 0 || z >= id)
+                                continue;
+                            for (int ky = 0; ky < kh; ky++) {
+                                int y = oy * stride[1] + ky * dil[1] - pad[2];
+                                if (y < 0 || y >= ih)
+                                    continue;
+                                for (int kx = 0; kx < kw; kx++) {
+                                    int xx = ox * stride[2] + kx * dil[2] - pad[4];
+                                    if (xx < 0 || xx >= iw)
+                                        continue;
+                                    int64_t xb = ((((int64_t)b * id + z) * ih + y) * iw + xx) * ic;
+                                    int64_t wb = ((((int64_t)co * kd + kz) * kh + ky) * kw + kx) * ic;
+                                    for (int c = 0; c < ic; c++) {
+                                        if (!is_int) {
+                                            accf = facc_mac(acc_kind, accf, xf[xb + c], wf[wb + c]);
+                                        } else if (acc_kind == ACC_I32) {
+                                            acc32 += (uint32_t)(int32_t)(xi[xb + c] - in_zp) *
+                                                     (uint32_t)(int32_t)(wi[wb + c] - w_zp);
+                                        } else {
+                                            acc64 += (uint64_t)(xi[xb + c] - in_zp) * (uint64_t)(wi[wb + c] - w_zp);
+                                        }
+                                    }
+                                }
+                            }
+                        }
+                        int bidx = bias_len == 1 ? 0 : co;
+                        if (!is_int)
+                            out_f[o++] = orc_round_to(out_fmt, orc_round_to(out_fmt, accf) + bf[bidx]);
+                        else if (acc_kind == ACC_I32)
+                            out_i[o++] = (int32_t)(acc32 + (uint32_t)(int32_t)bi[bidx]);
+                        else
+                            out_i[o++] = clamp48((int64_t)(acc64 + (uint64_t)bi[bidx]));
+                    }
+}
+
+/* TRANSPOSE_CONV2D: Transpose::accumulate, the gather form
+ * (src/ops/conv.rs:337-372: output (oy, ox) reads input
+ * ((oy - out_pad_top - ky) / sy, (ox - out_pad_left - kx) / sx) where the
+ * division is exact and in range; oc, then ky, kx, ic innermost) with
+ * eval_conv's epilogue (:457-496). x [N,IH,IW,IC], w [OC,KH,KW,IC];
+ * out_pad {top, bottom, left, right} (may be negative); output extent
+ * (I-1)*s + pad_a + pad_b + K (:302-304). Branches as orc_conv3d. */
+void orc_transpose_conv2d(int is_int, const int64_t *xi, const int64_t *wi, const int64_t *bi, const float *xf,
+                          const float *wf, const float *bf, int bias_len, int n, int ih, int iw, int ic, int oc,
+                          int kh, int kw, const int32_t *out_pad, const int32_t *stride, int64_t in_zp, int64_t w_zp,
+                          int acc_kind, int out_fmt, int64_t *out_i, float *out_f)
+{
+    int oh = (ih - 1) * stride[0] + out_pad[0] + out_pad[1] + kh;
+    int ow = (iw - 1) * stride[1] + out_pad[2] + out_pad[3] + kw;
+    int sy = stride[0], sx = stride[1];
+    int64_t o = 0;
+    for (int b = 0; b < n; b++)
+        for (int oy = 0; oy < oh; oy++) {
+            int iy = oy - out_pad[0];
+            for (int ox = 0; ox < ow; ox++) {
+                int ix = ox - out_pad[2];
+                for (int co = 0; co < oc; co++) {
+                    uint32_t acc32 = 0;
+                    uint64_t acc64 = 0;
+                    float accf = 0.0f;
+                    for (int ky = 0; ky < kh; ky++) {
+                        int y = iy - ky;
+                        if (y < 0 || y >= ih * sy || y % sy != 0)
+                            continue;
+                        for (int kx = 0; kx < kw; kx++) {
+                            int xx = ix - kx;
+                            if (xx < 0 || xx >= iw * sx || xx % sx != 0)
+                                continue;
+                            int64_t xb = (((int64_t)b * ih + y / sy) * iw + xx / sx) * ic;
+                            int64_t wb = (((int64_t)co * kh + ky) * kw + kx) * ic;
+                            for (int c = 0; c < ic; c++) {
+                                if (!is_int) {
+                                    accf = facc_mac(acc_kind, accf, xf[xb + c], wf[wb + c]);
+                                } else if (acc_kind == ACC_I32) {
+                                    acc32 += (uint32_t)(int32_t)(xi[xb + c] - in_zp) *
+                                             (uint32_t)(int32_t)(wi[wb + c] - w_zp);
+                                } else {
+                                    acc64 += (uint64_t)(xi[xb + c] - in_zp) * (uint64_t)(wi[wb + c] - w_zp);
+                                }
+                            }
+                        }
+                    }
+                    int bidx = bias_len == 1 ? 0 : co;
+                    if (!is_int)
+                        out_f[o++] = orc_round_to(out_fmt, orc_round_to(out_fmt, accf) + bf[bidx]);
+                    else if (acc_kind == ACC_I32)
+                        out_i[o++] = (int32_t)(acc32 + (uint32_t)(int32_t)bi[bidx]);
+                    else
+                        out_i[o++] = clamp48((int64_t)(acc64 + (uint64_t)bi[bidx]));
+                }
+            }
+        }
+}
+
 /* AVG_POOL2D integer: src/ops/pool.rs:193-214 with for_each_window (:77-104).
  * Returns ORC_ERR where apply_scale_32 would (a REQUIRE failure). */
 int orc_avg_pool_int(const int64_t *x, int n, int ih, int iw, int c, const int32_t *kernel, const int32_t *stride,

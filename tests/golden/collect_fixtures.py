@@ -14,12 +14,14 @@ import shutil
 import sys
 
 # Operators whose conformance cases are kept: the hot path (CONV2D,
-# DEPTHWISE_CONV2D, MATMUL, AVG_POOL2D, RESCALE) and the glue a quantised CNN
+# DEPTHWISE_CONV2D, MATMUL, AVG_POOL2D, RESCALE), the glue a quantised CNN
 # graph needs around it (CLAMP, ADD, RESHAPE, TRANSPOSE, CONST, CONST_SHAPE,
-# IDENTITY).
+# IDENTITY), and the operators next to the path on the same GEMM and pooling
+# cores (MATMUL_T, TRANSPOSE_CONV2D, CONV3D, MAX_POOL2D, CAST).
 OPS = [
     "conv2d", "depthwise_conv2d", "matmul", "avg_pool2d", "rescale",
     "clamp", "add", "reshape", "transpose", "const", "const_shape", "identity",
+    "matmul_t", "transpose_conv2d", "conv3d", "max_pool2d", "cast",
 ]
 
 

@@ -37,16 +37,16 @@ def run_product(c, strict=False, fusion=True):
 
 
 def mfma_float_op(c):
-    """The single CONV2D/MATMUL of a case that runs on float MFMA, or None."""
-    if c.tested_op() not in ("CONV2D", "MATMUL"):
+    """The single CONV2D/MATMUL/MATMUL_T of a case that runs on float MFMA, or None."""
+    if c.tested_op() not in ("CONV2D", "MATMUL", "MATMUL_T"):
         return None
-    op = [o for o in c.block.operators if o.op in ("CONV2D", "MATMUL")][0]
+    op = [o for o in c.block.operators if o.op in ("CONV2D", "MATMUL", "MATMUL_T")][0]
     a, b = (c.defs[op.inputs[0]].dtype, c.defs[op.inputs[1]].dtype)
     if (a, b) not in (("BF16", "BF16"), ("FP16", "FP16")):
         return None
     if op.op == "CONV2D" and op.attr.get("acc_type") != 7:  # FP32 accumulator
         return None
-    if op.op == "MATMUL" and c.defs[op.outputs[0]].dtype != "FP32":
+    if op.op in ("MATMUL", "MATMUL_T") and c.defs[op.outputs[0]].dtype != "FP32":
         return None
     return op
 
@@ -88,7 +88,7 @@ def tolerance(c, op, exp_vals, out_dt):
         del z
     else:
         K = g[0].shape[2]
-        s = O.matmul(g[0], g[1], 0, 0, "FP32")
+        s = (O.matmul_t if op.op == "MATMUL_T" else O.matmul)(g[0], g[1], 0, 0, "FP32")
         absum = s.vals.astype(np.float64).reshape(-1, 1)
         bterm = 0.0
     u = 2.0 ** -24

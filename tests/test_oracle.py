@@ -193,6 +193,109 @@ def test_conv2d_int_matches_bruteforce(seed):
     assert np.array_equal(got.vals.reshape(want.shape), want)
 
 
+def wrap32(v):
+    return ((v + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int64)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_conv3d_int_matches_bruteforce(seed):
+    # Depth slices of CONV3D are CONV2Ds: the 3-D sum equals the sum over kd
+    # of 2-D brute-force convolutions of the matching input depth slices.
+    rng = np.random.default_rng(700 + seed)
+    n, idp, ih, iw, ic, oc = 2, int(rng.integers(2, 6)), int(rng.integers(3, 7)), int(rng.integers(3, 7)), \
+        int(rng.integers(1, 6)), int(rng.integers(1, 5))
+    kd, kh, kw = int(rng.integers(1, 4)), int(rng.integers(1, 4)), int(rng.integers(1, 4))
+    stride = [int(v) for v in rng.integers(1, 3, size=3)]
+    dil = [int(v) for v in rng.integers(1, 3, size=3)]
+    pad = [int(v) for v in rng.integers(0, 3, size=6)]
+    for d, (i, k) in enumerate(((idp, kd), (ih, kh), (iw, kw))):
+        full = i - 1 + pad[2 * d] + pad[2 * d + 1] - (k - 1) * dil[d]
+        if full < 0:
+            pad[2 * d + 1] += -full
+            full = 0
+        pad[2 * d + 1] += (-full) % stride[d]
+    x = rng.integers(-128, 128, size=(n, idp, ih, iw, ic))
+    w = rng.integers(-128, 128, size=(oc, kd, kh, kw, ic))
+    bias = rng.integers(-2 ** 31, 2 ** 31, size=oc)
+    zx, zw = int(rng.integers(-128, 128)), int(rng.integers(-128, 128))
+    got = O.conv3d(O.T("INT8", x.shape, x), O.T("INT8", w.shape, w), O.T("INT32", bias.shape, bias), zx, zw,
+                   pad, stride, dil, "INT32")
+    od = (idp - 1 + pad[0] + pad[1] - (kd - 1) * dil[0]) // stride[0] + 1
+    oh = (ih - 1 + pad[2] + pad[3] - (kh - 1) * dil[1]) // stride[1] + 1
+    ow = (iw - 1 + pad[4] + pad[5] - (kw - 1) * dil[2]) // stride[2] + 1
+    want = None
+    for z in range(od):
+        plane = np.zeros((n, oh, ow, oc), dtype=np.int64)
+        for k in range(kd):
+            iz = z * stride[0] + k * dil[0] - pad[0]
+            if not 0 <= iz < idp:
+                continue
+            # a 2-D convolution of this depth slice with the k-th kernel plane
+            # (zero bias, unwrapped: the sum is wrapped once at the end)
+            c2 = conv_bruteforce(x[:, iz], w[:, k], np.zeros(oc, np.int64), zx, zw, pad[2:], stride[1:], dil[1:])
+            plane = plane + c2
+        acc = np.asarray(plane, dtype=np.int64) + bias.astype(np.int64)
+        want = acc[:, None] if want is None else np.concatenate([want, acc[:, None]], axis=1)
+    # conv_bruteforce wraps each partial sum to int32; wrapping is additive mod 2^32
+    assert np.array_equal(wrap32(got.vals), wrap32(want.reshape(-1)))
+    assert got.shape == [n, od] + list(want.shape[2:])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_transpose_conv2d_int_matches_scatter_form(seed):
+    # The reference gathers (output reads input where (o - pad - k) / s is
+    # exact); the scatter form adds every input pixel's products into output
+    # (i s + k + pad), dropping what falls outside a cropped (negative pad)
+    # output.
+    rng = np.random.default_rng(800 + seed)
+    n, ih, iw, ic, oc = 2, int(rng.integers(2, 6)), int(rng.integers(2, 6)), int(rng.integers(1, 6)), \
+        int(rng.integers(1, 5))
+    kh, kw = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+    stride = [int(rng.integers(1, 4)), int(rng.integers(1, 4))]
+    out_pad = [int(rng.integers(-kh + 1, 3)), int(rng.integers(-kh + 1, 3)), int(rng.integers(-kw + 1, 3)),
+               int(rng.integers(-kw + 1, 3))]
+    oh = (ih - 1) * stride[0] + out_pad[0] + out_pad[1] + kh
+    ow = (iw - 1) * stride[1] + out_pad[2] + out_pad[3] + kw
+    if oh < 1 or ow < 1:
+        pytest.skip("empty output for this draw")
+    x = rng.integers(-128, 128, size=(n, ih, iw, ic))
+    w = rng.integers(-128, 128, size=(oc, kh, kw, ic))
+    bias = rng.integers(-2 ** 31, 2 ** 31, size=oc)
+    zx, zw = int(rng.integers(-128, 128)), int(rng.integers(-128, 128))
+    got = O.transpose_conv2d(O.T("INT8", x.shape, x), O.T("INT8", w.shape, w), O.T("INT32", bias.shape, bias), zx,
+                             zw, out_pad, stride, "INT32")
+    want = np.zeros((n, oh, ow, oc), dtype=np.int64)
+    xs, ws = x.astype(np.int64) - zx, w.astype(np.int64) - zw
+    for y in range(ih):
+        for xx in range(iw):
+            for ky in range(kh):
+                for kx in range(kw):
+                    oy, ox = y * stride[0] + ky + out_pad[0], xx * stride[1] + kx + out_pad[2]
+                    if 0 <= oy < oh and 0 <= ox < ow:
+                        want[:, oy, ox, :] += xs[:, y, xx, :] @ ws[:, ky, kx, :].T
+    want += bias.astype(np.int64)
+    assert got.shape == [n, oh, ow, oc]
+    assert np.array_equal(got.vals, wrap32(want.reshape(-1)))
+
+
+def test_max_pool_and_cast_known_answers():
+    # MAX_POOL2D: padding never wins (a window of negatives next to the pad
+    # keeps its own maximum), ties keep the running value (-0 before +0), NaN
+    # per mode; CAST: saturation at the FP16-rounded INT16 bound 32768 and
+    # round half to even.
+    x = np.array([-5.0, -3.0, -0.0, 0.0, np.nan, 2.0], np.float32).reshape(1, 1, 6, 1)
+    t = O.T("FP32", [1, 1, 6, 1], x.reshape(-1))
+    prop = O.max_pool2d(t, [1, 2], [1, 2], [0, 0, 0, 0], 1).vals
+    ign = O.max_pool2d(t, [1, 2], [1, 2], [0, 0, 0, 0], 2).vals
+    assert prop[0] == -3.0 and np.signbit(prop[1]) and np.isnan(prop[2])
+    assert ign[0] == -3.0 and ign[2] == 2.0
+    padded = O.max_pool2d(O.T("INT8", [1, 1, 2, 1], np.array([-7, -9])), [1, 2], [1, 1], [0, 0, 1, 0], 1).vals
+    assert list(padded) == [-7, -7]
+    h = O.T("FP16", [6], np.array([32767.0, 40000.0, -40000.0, 2.5, 3.5, -2.5], np.float32))
+    assert list(O.cast(h, "INT16").vals) == [32767, 32767, -32768, 2, 4, -2]
+    assert list(O.cast(O.T("INT32", [2], np.array([300, -129])), "INT8").vals) == [44, 127]
+
+
 @pytest.mark.parametrize("seed", range(8))
 def test_depthwise_int_matches_bruteforce(seed):
     rng = np.random.default_rng(200 + seed)

@@ -74,7 +74,8 @@ FusionPlan FusionPlan::build(const BasicBlock& b)
     };
     for (size_t i = 0; i < n; i++) {
         const Operator& o = b.operators[i];
-        if ((o.op == OP_CONV2D || o.op == OP_DEPTHWISE_CONV2D || o.op == OP_MATMUL) && o.outputs.size() == 1) {
+        if ((o.op == OP_CONV2D || o.op == OP_DEPTHWISE_CONV2D || o.op == OP_MATMUL || o.op == OP_MATMUL_T) &&
+            o.outputs.size() == 1) {
             const int j = sole_first_use(o.outputs[0], OP_RESCALE);
             if (j >= 0) {
                 p.rescale_after[i] = j;

@@ -242,6 +242,12 @@ enum ElemCode : int32_t {
 struct DirectConvDesc {
     int32_t depthwise = 0;
     int32_t n, ih, iw, c, m, oc, kh, kw, oh, ow, pt, pl, sy, sx, dy, dx;  // c = input channels, m = multiplier
+    // CONV3D: the depth dimension (input id, kernel kd, output od, front pad
+    // pf, stride sz, dilation dz); 1/0 for the 2-D convolutions.
+    int32_t id = 1, kd = 1, od = 1, pf = 0, sz = 1, dz = 1;
+    // TRANSPOSE_CONV2D (gather form): pt/pl are out_pad top/left (possibly
+    // negative), sy/sx the strides; dy/dx unused.
+    int32_t transpose = 0;
     ElemCode xe, we, be, oe;  // input, weight, bias and output element codes
     AccKind acc;
     int64_t zp_x = 0, zp_w = 0;   // integer zero points
@@ -254,6 +260,8 @@ void direct_conv(const DirectConvDesc& d, const void* x, const void* w, const vo
 
 struct DirectMatmulDesc {
     int32_t batch, h, c, w;
+    int32_t b_transposed = 0;  // MATMUL_T: b is [D][w][c] rather than [batch][c][w]
+    int32_t b_broadcast = 0;   // MATMUL_T with D = 1: every batch reads b's only slice
     ElemCode ae, be, oe;
     AccKind acc;
     int64_t zp_a = 0, zp_b = 0;
@@ -289,6 +297,23 @@ struct PoolDesc {
     int32_t out_fmt = FMT_F32;                       // float path: output encoding
 };
 void avg_pool2d(const PoolDesc& d, const void* x, void* out, uint32_t* err, hipStream_t stream);
+// MAX_POOL2D (xe int8/int16 or a float code; out in the same type): `ignore`
+// selects NaN mode IGNORE, `lowest` is the float type's lowest value.
+void max_pool2d(const PoolDesc& d, bool ignore, float lowest, const void* x, void* out, hipStream_t stream);
+
+// CAST between the element types (src/ops/type_conv.rs:45-80): from/to
+// element codes, `from_float` / `to_float` tell integer (BOOL: E_U8) from
+// float codes, `to_bool` marks a BOOL result, to_fmt the float output
+// format; float -> int saturates at hi/lo when the value reaches hi_bound /
+// lo_bound (the bounds rounded to the input's precision).
+struct CastDesc {
+    ElemCode from, to;
+    int32_t from_float = 0, to_float = 0, to_bool = 0;
+    int32_t to_fmt = FMT_F32;
+    int64_t lo = 0, hi = 0;
+    float lo_bound = 0, hi_bound = 0;
+};
+void cast(const CastDesc& d, const void* x, int64_t count, void* out, hipStream_t stream);
 
 // Standalone RESCALE over `count` elements of element code `xe`.
 void rescale(const RescaleDev& rs, ElemCode xe, const void* x, int64_t count, void* out, uint32_t* err,

@@ -486,6 +486,91 @@ unsigned grid_for(int64_t n)
     return static_cast<unsigned>(b < 65536 ? (b < 1 ? 1 : b) : 65536);
 }
 
+
+// MAX_POOL2D (src/ops/pool.rs:233-286): one output per thread; the window's
+// in-bounds positions in (ky, kx) order (for_each_window, :77-104).
+// Integers fold max from the type's minimum; floats fold nan_max
+// (src/ops/common.rs:155-177: ties keep the running value, NaN handled per
+// mode) from the type's lowest value, or from NaN under IGNORE.
+__global__ void max_pool_kernel(PoolDesc d, bool ignore, float lowest, const void* x, void* out, int64_t total)
+{
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total)
+        return;
+    const int c = int(idx % d.c);
+    int64_t r = idx / d.c;
+    const int ox = int(r % d.ow);
+    r /= d.ow;
+    const int oy = int(r % d.oh);
+    const int b = int(r / d.oh);
+    const int iy = oy * d.sy - d.pt, ix = ox * d.sx - d.pl;
+    const bool is_int = d.xe == E_I8 || d.xe == E_I16;
+    int64_t mi = d.xe == E_I8 ? -128 : -32768;
+    float mf = ignore ? __builtin_nanf("") : lowest;
+    for (int ky = 0; ky < d.kh; ky++) {
+        const int y = iy + ky;
+        if (y < 0 || y >= d.ih)
+            continue;
+        for (int kx = 0; kx < d.kw; kx++) {
+            const int xx = ix + kx;
+            if (xx < 0 || xx >= d.iw)
+                continue;
+            const int64_t i = ((int64_t(b) * d.ih + y) * d.iw + xx) * d.c + c;
+            if (is_int) {
+                const int64_t v = load_int(x, i, d.xe);
+                mi = v > mi ? v : mi;
+            } else {
+                const float v = load_float(x, i, d.xe);
+                if (__builtin_isnan(mf) || __builtin_isnan(v))
+                    mf = ignore ? (__builtin_isnan(mf) ? v : mf) : __builtin_nanf("");
+                else
+                    mf = mf >= v ? mf : v;
+            }
+        }
+    }
+    if (is_int)
+        store_int(out, idx, d.xe, mi);
+    else
+        store_float(out, idx, d.out_fmt, mf);
+}
+
+// CAST (src/ops/type_conv.rs:45-80), one element per thread.
+__global__ void cast_kernel(CastDesc d, const void* x, int64_t count, void* out)
+{
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= count)
+        return;
+    if (!d.from_float) {
+        const int64_t v = load_int(x, i, d.from);  // BOOL reads as 0 / 1
+        if (d.to_bool)
+            store_int(out, i, E_U8, v != 0 ? 1 : 0);
+        else if (d.to_float)
+            store_float(out, i, d.to_fmt, float(v));  // through FP32, then to the format
+        else
+            store_int(out, i, d.to, v);  // wraps (int_data)
+        return;
+    }
+    const float v = load_float(x, i, d.from);
+    if (d.to_bool) {
+        store_int(out, i, E_U8, v != 0.0f ? 1 : 0);
+    } else if (d.to_float) {
+        store_float(out, i, d.to_fmt, v);
+    } else {
+        // float_to_int (:34-43): saturate at the bounds as rounded to the
+        // input's precision, else round half to even; NaN becomes 0.
+        int64_t q;
+        if (v >= d.hi_bound)
+            q = d.hi;
+        else if (v <= d.lo_bound)
+            q = d.lo;
+        else if (__builtin_isnan(v))
+            q = 0;
+        else
+            q = int64_t(__builtin_rintf(v));
+        store_int(out, i, d.to, q);
+    }
+}
+
 }  // namespace
 
 // The residual kernel without per-element checks applies when every REQUIRE
@@ -552,6 +637,20 @@ void avg_pool2d(const PoolDesc& d, const void* x, void* out, uint32_t* err, hipS
     } else {
         hipLaunchKernelGGL(avg_pool_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, d, x, out, err, total);
     }
+}
+
+void max_pool2d(const PoolDesc& d, bool ignore, float lowest, const void* x, void* out, hipStream_t stream)
+{
+    const int64_t total = int64_t(d.n) * d.oh * d.ow * d.c;
+    if (total > 0)
+        hipLaunchKernelGGL(max_pool_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, d, ignore, lowest, x,
+                           out, total);
+}
+
+void cast(const CastDesc& d, const void* x, int64_t count, void* out, hipStream_t stream)
+{
+    if (count > 0)
+        hipLaunchKernelGGL(cast_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, d, x, count, out);
 }
 
 void rescale(const RescaleDev& rs, ElemCode xe, const void* x, int64_t count, void* out, uint32_t* err,

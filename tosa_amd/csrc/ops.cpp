@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <limits>
 #include <mutex>
 #include <optional>
 
@@ -1164,6 +1165,22 @@ bool matmul_types(DType a, DType b, DType out)
     return false;
 }
 
+// MATMUL_T's (a, b, output) combinations (src/ops/matmul.rs:40-51): any mix
+// of FP8/FP16/BF16/FP32 operands into BF16 or FP32 (FP32 operands need an
+// FP32 output), plus the integer pairs and FP16 x FP16 -> FP16.
+bool matmul_t_types(DType a, DType b, DType out)
+{
+    auto fl = [](DType t) { return is_fp8(t) || t == DT_FP16 || t == DT_BF16 || t == DT_FP32; };
+    if ((a == DT_INT8 && b == DT_INT8 && out == DT_INT32) || (a == DT_INT16 && b == DT_INT16 && out == DT_INT48) ||
+        (a == DT_FP16 && b == DT_FP16 && out == DT_FP16))
+        return true;
+    if (out == DT_FP32)
+        return fl(a) && fl(b);
+    if (out == DT_BF16)
+        return fl(a) && fl(b) && a != DT_FP32 && b != DT_FP32 && !(a == DT_FP16 && b == DT_FP16);
+    return false;
+}
+
 DType matmul_default_output(DType a)
 {
     switch (a) {
@@ -1176,9 +1193,11 @@ DType matmul_default_output(DType a)
     }
 }
 
-void eval_matmul(ExecState& st, const Operator& op, size_t index)
+// MATMUL (transposed false) and MATMUL_T (true): b [N,C,W], or b [D,W,C]
+// with D = N or 1 (broadcast). src/ops/matmul.rs:98-182.
+void eval_matmul(ExecState& st, const Operator& op, size_t index, bool transposed)
 {
-    const std::string OP = "MATMUL";
+    const std::string OP = transposed ? "MATMUL_T" : "MATMUL";
     expect_operands(op, OP, 4, 1);
     auto a = st.get(op.inputs[0]);
     auto b = st.get(op.inputs[1]);
@@ -1188,14 +1207,16 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
     expect_rank(OP, "a", *a, 3);
     expect_rank(OP, "b", *b, 3);
     const int64_t n = a->shape[0], h = a->shape[1], c = a->shape[2];
-    const int64_t bn = b->shape[0], bc = b->shape[1], w = b->shape[2];
-    if (bc != c || bn != n)
+    const int64_t bn = b->shape[0], bc = transposed ? b->shape[2] : b->shape[1];
+    const int64_t w = transposed ? b->shape[1] : b->shape[2];
+    if (bc != c || (bn != n && !(transposed && bn == 1)))
         throw Error(ERR_SHAPE_MISMATCH, OP + ": b shape " + shape_str(b->shape) + " incompatible with a shape " +
                                             shape_str(a->shape));
+    const bool broadcast = bn != n;
     const Shape out_shape = {n, h, w};
     const DType a_t = a->dtype(), b_t = b->dtype();
     const DType out_t = check_declared_output(st, OP, out_name, out_shape).value_or(matmul_default_output(a_t));
-    if (!matmul_types(a_t, b_t, out_t))
+    if (!(transposed ? matmul_t_types : matmul_types)(a_t, b_t, out_t))
         throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported types a=" + dtype_name(a_t) + " b=" + dtype_name(b_t) +
                                             " output=" + dtype_name(out_t));
     if (a_zp->dtype() != a_t || b_zp->dtype() != b_t)
@@ -1217,31 +1238,40 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
     const bool mfma_float = !is_int && out_t == DT_FP32 && !st.opts.strict_float && small &&
                             ((a_t == DT_BF16 && b_t == DT_BF16) || (a_t == DT_FP16 && b_t == DT_FP16));
     const void* a_dev = (mfma_int && c % 16 == 0) ? a->data->device_in() : nullptr;
-    if (a_dev && reinterpret_cast<uintptr_t>(a_dev) % 16 == 0) {
+    const void* b_dev = transposed && a_dev ? b->data->device_in() : nullptr;
+    if (a_dev && reinterpret_cast<uintptr_t>(a_dev) % 16 == 0 &&
+        (!transposed || reinterpret_cast<uintptr_t>(b_dev) % 16 == 0)) {
         // int8: the pointwise tiled kernel, one batch per grid slice, over B
-        // transposed to rows of c bytes (cached when B is a graph constant);
-        // zero points folded into the accumulator like CONV2D's.
+        // as rows of c bytes: MATMUL_T's own layout, or MATMUL's B transposed
+        // (cached when B is a graph constant); zero points folded into the
+        // accumulator like CONV2D's. A MATMUL_T B shared by every batch
+        // makes the batches one problem of n h rows.
         const bool b_const = st.is_const(op.inputs[1]);
         ConvI8Desc fd;
         fd.x = static_cast<const int8_t*>(a_dev);
         fd.bias = nullptr;
         fd.bias_len = 1;
         fd.n = 1;
-        fd.ih = fd.oh = int32_t(h);
+        fd.ih = fd.oh = int32_t(broadcast ? n * h : h);
         fd.iw = fd.ow = 1;
         fd.ic = int32_t(c);
         fd.oc = int32_t(w);
         fd.zp_x = int32_t(azp);
         fd.zp_w = int32_t(bzp);
-        fd.batch = int32_t(n);
-        auto launch = [fd, a, b, b_const](void* out, const RescaleDev* rs, bool rs_const, uint32_t* err,
-                                          hipStream_t s) {
+        fd.batch = int32_t(broadcast ? 1 : n);
+        auto launch = [fd, a, b, b_const, transposed](void* out, const RescaleDev* rs, bool rs_const, uint32_t* err,
+                                                      hipStream_t s) {
             ConvI8Desc d = fd;
-            auto bt = derived_i8(*b->data, "matmul_bt", int64_t(d.batch) * d.ic * d.oc, b_const, s, [&](void* dst) {
-                transpose_b_i8(static_cast<const int8_t*>(b->data->device_in()), d.batch, d.ic, d.oc,
-                               static_cast<int8_t*>(dst), s);
-            });
-            d.w = static_cast<const int8_t*>(bt->device_in());
+            StoragePtr bt;
+            if (transposed) {
+                d.w = static_cast<const int8_t*>(b->data->device_in());
+            } else {
+                bt = derived_i8(*b->data, "matmul_bt", int64_t(d.batch) * d.ic * d.oc, b_const, s, [&](void* dst) {
+                    transpose_b_i8(static_cast<const int8_t*>(b->data->device_in()), d.batch, d.ic, d.oc,
+                                   static_cast<int8_t*>(dst), s);
+                });
+                d.w = static_cast<const int8_t*>(bt->device_in());
+            }
             auto tab = conv_i8_table_for(d, *b->data, nullptr, rs, b_const && (!rs || rs_const), s);
             d.range_safe = tab->scale_range_safe;
             conv_i8_fast(d, tab->device_in(), rs, out, err, s);
@@ -1271,22 +1301,23 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
         st.set(out);
         return;
     }
+    const int64_t fbatch = broadcast ? 1 : n, fm = broadcast ? n * h : h;
     if (mfma_float && count > 0 &&
-        kern::gemm_f16_supported(n, h, w, c, true, a->data->device_in(), b->data->device_in())) {
+        kern::gemm_f16_supported(fbatch, fm, w, c, !transposed, a->data->device_in(), b->data->device_in())) {
         GemmF16Desc fd;
-        fd.batch = int32_t(n);
-        fd.m = int32_t(h);
+        fd.batch = int32_t(fbatch);
+        fd.m = int32_t(fm);
         fd.n = int32_t(w);
         fd.k = int32_t(c);
         fd.elem = a_t == DT_BF16 ? ELEM_BF16 : ELEM_F16;
-        fd.b_kn = true;
+        fd.b_kn = !transposed;
         fd.out_fmt = FMT_F32;
         auto out = new_output(out_name, out_shape, out_t);
         kern::gemm_f16(fd, a->data->device_in(), b->data->device_in(), out->data->device_out(), st.s());
         st.set(out);
         return;
     }
-    if (mfma_int || mfma_float) {
+    if ((mfma_int || mfma_float) && !transposed) {
         GemmDesc gd;
         gd.is_conv = 0;
         gd.elem = mfma_int ? ELEM_I8 : (a_t == DT_BF16 ? ELEM_BF16 : ELEM_F16);
@@ -1332,6 +1363,8 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
     d.h = int32_t(h);
     d.c = int32_t(c);
     d.w = int32_t(w);
+    d.b_transposed = transposed ? 1 : 0;
+    d.b_broadcast = broadcast ? 1 : 0;
     d.ae = elem_code(a_t);
     d.be = elem_code(b_t);
     d.oe = elem_code(out_t);
@@ -1352,20 +1385,12 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index)
 // ---------------------------------------------------------------------------
 // AVG_POOL2D (src/ops/pool.rs:17-105, :146-231)
 // ---------------------------------------------------------------------------
-void eval_avg_pool2d(ExecState& st, const Operator& op)
+// PoolGeometry::new (src/ops/pool.rs:30-70): shared by AVG_POOL2D and
+// MAX_POOL2D. Fills the geometry fields of a PoolDesc.
+PoolDesc pool_geometry(const std::string& OP, const Tensor& input, const std::vector<int32_t>& kernel,
+                       const std::vector<int32_t>& stride, const std::vector<int32_t>& pad)
 {
-    const std::string OP = "AVG_POOL2D";
-    if (op.attr.kind != AttrKind::Pool2d)
-        throw invalid(OP, "missing attribute");
-    const auto& kernel = op.attr.kernel;
-    const auto& stride = op.attr.stride;
-    const auto& pad = op.attr.pad;
-    const DType acc_t = op.attr.acc_type;
-    expect_operands(op, OP, 3, 1);
-    auto input = st.get(op.inputs[0]);
-    auto izp = single_value(OP, "input_zp", st.get(op.inputs[1]));
-    auto ozp = single_value(OP, "output_zp", st.get(op.inputs[2]));
-    expect_rank(OP, "input", *input, 4);
+    expect_rank(OP, "input", input, 4);
     if (pad.size() != 4 || kernel.size() != 2 || stride.size() != 2)
         throw invalid(OP, "pad must have 4 elements, kernel and stride 2");
     for (int32_t p : pad)
@@ -1379,7 +1404,7 @@ void eval_avg_pool2d(ExecState& st, const Operator& op)
             throw invalid(OP, "kernel and stride must be at least 1");
     if (pad[0] >= kernel[0] || pad[1] >= kernel[0] || pad[2] >= kernel[1] || pad[3] >= kernel[1])
         throw invalid(OP, "pad must be smaller than kernel");
-    const int64_t n = input->shape[0], ih = input->shape[1], iw = input->shape[2], c = input->shape[3];
+    const int64_t n = input.shape[0], ih = input.shape[1], iw = input.shape[2], c = input.shape[3];
     if (ih == 0 || iw == 0)
         throw invalid(OP, "input height and width must be positive");
     auto extent = [&](int64_t size, int32_t a, int32_t b, int32_t k, int32_t s) {
@@ -1390,6 +1415,39 @@ void eval_avg_pool2d(ExecState& st, const Operator& op)
     };
     const int64_t oh = extent(ih, pad[0], pad[1], kernel[0], stride[0]);
     const int64_t ow = extent(iw, pad[2], pad[3], kernel[1], stride[1]);
+    if (n * ih * iw * c >= (int64_t(1) << 31) || n * oh * ow * c >= (int64_t(1) << 31))
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": tensors of 2^31 elements or more are not supported");
+    PoolDesc d{};
+    d.n = int32_t(n);
+    d.ih = int32_t(ih);
+    d.iw = int32_t(iw);
+    d.c = int32_t(c);
+    d.kh = kernel[0];
+    d.kw = kernel[1];
+    d.oh = int32_t(oh);
+    d.ow = int32_t(ow);
+    d.pt = pad[0];
+    d.pl = pad[2];
+    d.sy = stride[0];
+    d.sx = stride[1];
+    return d;
+}
+
+void eval_avg_pool2d(ExecState& st, const Operator& op)
+{
+    const std::string OP = "AVG_POOL2D";
+    if (op.attr.kind != AttrKind::Pool2d)
+        throw invalid(OP, "missing attribute");
+    const auto& kernel = op.attr.kernel;
+    const auto& stride = op.attr.stride;
+    const auto& pad = op.attr.pad;
+    const DType acc_t = op.attr.acc_type;
+    expect_operands(op, OP, 3, 1);
+    auto input = st.get(op.inputs[0]);
+    auto izp = single_value(OP, "input_zp", st.get(op.inputs[1]));
+    auto ozp = single_value(OP, "output_zp", st.get(op.inputs[2]));
+    const PoolDesc g = pool_geometry(OP, *input, kernel, stride, pad);
+    const int64_t n = g.n, ih = g.ih, iw = g.iw, c = g.c, oh = g.oh, ow = g.ow;
     const Shape out_shape = {n, oh, ow, c};
     const DType in_t = input->dtype();
     auto declared = check_declared_output(st, OP, op.outputs[0], out_shape);
@@ -1405,19 +1463,7 @@ void eval_avg_pool2d(ExecState& st, const Operator& op)
                     OP + ": unsupported types input=" + dtype_name(in_t) + " acc=" + dtype_name(acc_t));
     if (izp->dtype() != in_t || ozp->dtype() != in_t)
         throw Error(ERR_DTYPE_MISMATCH, OP + ": zero points must have the input dtype");
-    PoolDesc d{};
-    d.n = int32_t(n);
-    d.ih = int32_t(ih);
-    d.iw = int32_t(iw);
-    d.c = int32_t(c);
-    d.kh = kernel[0];
-    d.kw = kernel[1];
-    d.oh = int32_t(oh);
-    d.ow = int32_t(ow);
-    d.pt = pad[0];
-    d.pl = pad[2];
-    d.sy = stride[0];
-    d.sx = stride[1];
+    PoolDesc d = g;
     d.xe = elem_code(in_t);
     if (dtype_is_int(in_t)) {
         const int64_t iz = int_values(*izp)[0], oz = int_values(*ozp)[0];
@@ -1449,6 +1495,288 @@ struct RescaleRecipe {
     TensorPtr src;
     RescalePrep rp;
 };
+
+// ---------------------------------------------------------------------------
+// MAX_POOL2D (src/ops/pool.rs:233-286)
+// ---------------------------------------------------------------------------
+void eval_max_pool2d(ExecState& st, const Operator& op)
+{
+    const std::string OP = "MAX_POOL2D";
+    if (op.attr.kind != AttrKind::Pool2d)
+        throw invalid(OP, "missing attribute");
+    expect_operands(op, OP, 1, 1);
+    if (op.attr.nan_mode == NAN_UNKNOWN)
+        throw invalid(OP, "nan_mode must be PROPAGATE or IGNORE");
+    auto input = st.get(op.inputs[0]);
+    PoolDesc d = pool_geometry(OP, *input, op.attr.kernel, op.attr.stride, op.attr.pad);
+    const Shape out_shape = {d.n, d.oh, d.ow, d.c};
+    const DType in_t = input->dtype();
+    auto declared = check_declared_output(st, OP, op.outputs[0], out_shape);
+    if (declared && *declared != in_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": output dtype " + dtype_name(*declared) + " must match input dtype " +
+                                            dtype_name(in_t));
+    const bool ok = in_t == DT_INT8 || in_t == DT_INT16 || in_t == DT_FP16 || in_t == DT_BF16 || in_t == DT_FP32 ||
+                    is_fp8(in_t);
+    if (!ok)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported dtype " + dtype_name(in_t));
+    d.xe = elem_code(in_t);
+    d.out_fmt = fmt_code(in_t);
+    // float_lowest (src/ops/common.rs:136-140)
+    const float lowest = in_t == DT_FP8E4M3 ? -448.0f : -std::numeric_limits<float>::infinity();
+    auto out = new_output(op.outputs[0], out_shape, in_t);
+    void* od = out->data->device_out();
+    if (shape_count(out_shape) > 0)
+        kern::max_pool2d(d, op.attr.nan_mode == NAN_IGNORE, lowest, input->data->device_in(), od, st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// CAST (src/ops/type_conv.rs:14-80)
+// ---------------------------------------------------------------------------
+// cast_supported (:14-28): the reference model's CAST pairs.
+bool cast_supported(DType from, DType to)
+{
+    auto is = [](DType t, std::initializer_list<DType> l) {
+        for (DType u : l)
+            if (u == t)
+                return true;
+        return false;
+    };
+    const auto fl16 = {DT_FP16, DT_BF16, DT_FP32};
+    if (from == DT_BOOL)
+        return is(to, {DT_INT8, DT_INT16, DT_INT32, DT_INT64, DT_FP32});
+    if (to == DT_BOOL)
+        return is(from, {DT_INT8, DT_INT16, DT_INT32, DT_INT64, DT_FP32});
+    if ((from == DT_INT8 && is(to, {DT_INT16, DT_INT32})) || (from == DT_INT16 && is(to, {DT_INT8, DT_INT32})) ||
+        (from == DT_INT32 && is(to, {DT_INT8, DT_INT16, DT_INT64})) || (from == DT_INT64 && to == DT_INT32))
+        return true;
+    if (is(from, {DT_INT8, DT_INT16, DT_INT32}) && is(to, fl16))
+        return true;
+    if (is(from, fl16) && is(to, {DT_INT8, DT_INT16, DT_INT32}))
+        return true;
+    if ((is(from, {DT_FP16, DT_BF16}) && to == DT_FP32) || (from == DT_FP32 && is(to, {DT_FP16, DT_BF16})))
+        return true;
+    if (is(from, fl16) && is_fp8(to))
+        return true;
+    if (is_fp8(from) && is(to, fl16))
+        return true;
+    return false;
+}
+
+// round_to (src/ops/common.rs:100-108) on the host, for the formats CAST
+// converts to integers from (FP16, BF16, FP32): the saturation bounds are
+// compared in the input's precision (:34-43). Round to nearest, ties to
+// even; FP16 overflows to infinity from 65520.
+float round_to_format(DType t, float x)
+{
+    if (t == DT_FP32 || !std::isfinite(x))
+        return x;
+    if (t == DT_BF16) {
+        uint32_t u;
+        std::memcpy(&u, &x, 4);
+        u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+        float r;
+        std::memcpy(&r, &u, 4);
+        return r;
+    }
+    if (t != DT_FP16)
+        throw Error(ERR_DTYPE_MISMATCH, std::string("round_to_format: ") + dtype_name(t));
+    const float a = std::fabs(x);
+    if (a >= 65520.0f)
+        return std::copysign(std::numeric_limits<float>::infinity(), x);
+    int e = 0;
+    std::frexp(a, &e);
+    const float q = std::ldexp(1.0f, std::max(e, -13) - 11);  // 11 significant bits; subnormal quantum 2^-24
+    return std::nearbyint(x / q) * q;
+}
+
+void eval_cast(ExecState& st, const Operator& op)
+{
+    const std::string OP = "CAST";
+    expect_operands(op, OP, 1, 1);
+    auto input = st.get(op.inputs[0]);
+    const DType from = input->dtype();
+    auto declared = check_declared_output(st, OP, op.outputs[0], input->shape);
+    if (!declared)
+        throw invalid(OP, "output type must be declared");
+    const DType to = *declared;
+    if (!cast_supported(from, to))
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported cast " + dtype_name(from) + " -> " + dtype_name(to));
+    CastDesc d{};
+    d.from = elem_code(from);
+    d.to = elem_code(to);
+    d.from_float = dtype_is_int(from) || from == DT_BOOL ? 0 : 1;
+    d.to_bool = to == DT_BOOL ? 1 : 0;
+    d.to_float = dtype_is_int(to) || to == DT_BOOL ? 0 : 1;
+    d.to_fmt = fmt_code(to);
+    if (d.from_float && !d.to_float && !d.to_bool) {
+        auto [lo, hi] = int_range(to);
+        d.lo = lo;
+        d.hi = hi;
+        d.lo_bound = round_to_format(from, float(lo));
+        d.hi_bound = round_to_format(from, float(hi));
+    }
+    auto out = new_output(op.outputs[0], input->shape, to);
+    const int64_t count = shape_count(input->shape);
+    void* od = out->data->device_out();
+    if (count > 0)
+        kern::cast(d, input->data->device_in(), count, od, st.s());
+    st.set(out);
+}
+
+// ---------------------------------------------------------------------------
+// CONV3D and TRANSPOSE_CONV2D (src/ops/conv.rs:505-511, :526-532): eval_conv
+// (:398-500) over ConvNd with three spatial dimensions (:92-181) or the
+// gather-form Transpose (:268-372), on the reference-order kernel.
+// ---------------------------------------------------------------------------
+void eval_conv_nd(ExecState& st, const Operator& op, bool transpose)
+{
+    const std::string OP = transpose ? "TRANSPOSE_CONV2D" : "CONV3D";
+    if (op.attr.kind != (transpose ? AttrKind::TransposeConv2d : AttrKind::Conv3d))
+        throw invalid(OP, "missing attribute");
+    expect_operands(op, OP, 5, 1);
+    auto input = st.get(op.inputs[0]);
+    auto weight = st.get(op.inputs[1]);
+    auto bias = st.get(op.inputs[2]);
+    auto in_zp = single_value(OP, "input_zp", st.get(op.inputs[3]));
+    auto w_zp = single_value(OP, "weight_zp", st.get(op.inputs[4]));
+    expect_rank(OP, "bias", *bias, 1);
+    DirectConvDesc d{};
+    d.m = 1;
+    d.dy = d.dx = 1;
+    Shape out_shape;
+    if (transpose) {
+        // Transpose::new (:284-330)
+        expect_rank(OP, "input", *input, 4);
+        expect_rank(OP, "weight", *weight, 4);
+        const auto& out_pad = op.attr.out_pad;
+        const auto& stride = op.attr.stride;
+        if (out_pad.size() != 4 || stride.size() != 2)
+            throw invalid(OP, "out_pad must have 4 elements and stride 2");
+        for (int32_t sv : stride)
+            if (sv < 1)
+                throw invalid(OP, "stride must be at least 1");
+        const int64_t n = input->shape[0], ih = input->shape[1], iw = input->shape[2], ic = input->shape[3];
+        const int64_t oc = weight->shape[0], kh = weight->shape[1], kw = weight->shape[2];
+        if (weight->shape[3] != ic)
+            throw Error(ERR_SHAPE_MISMATCH, OP + ": weight input channels " + std::to_string(weight->shape[3]) +
+                                                " != input channels " + std::to_string(ic));
+        for (size_t i = 0; i < 4; i++)
+            if (int64_t(out_pad[i]) <= -(i < 2 ? kh : kw))
+                throw invalid(OP, "out_pad must be greater than -kernel size");
+        const int64_t oh = (ih - 1) * stride[0] + out_pad[0] + out_pad[1] + kh;
+        const int64_t ow = (iw - 1) * stride[1] + out_pad[2] + out_pad[3] + kw;
+        if (oh < 1 || ow < 1)
+            throw invalid(OP, "output size " + std::to_string(oh) + "x" + std::to_string(ow) + " must be positive");
+        d.transpose = 1;
+        d.n = int32_t(n);
+        d.ih = int32_t(ih);
+        d.iw = int32_t(iw);
+        d.c = int32_t(ic);
+        d.oc = int32_t(oc);
+        d.kh = int32_t(kh);
+        d.kw = int32_t(kw);
+        d.oh = int32_t(oh);
+        d.ow = int32_t(ow);
+        d.pt = out_pad[0];
+        d.pl = out_pad[2];
+        d.sy = stride[0];
+        d.sx = stride[1];
+        out_shape = {n, oh, ow, oc};
+    } else {
+        // ConvNd::new with three dimensions (:106-139)
+        expect_rank(OP, "input", *input, 5);
+        expect_rank(OP, "weight", *weight, 5);
+        const auto& pad = op.attr.pad;
+        const auto& stride = op.attr.stride;
+        const auto& dil = op.attr.dilation;
+        if (pad.size() != 6 || stride.size() != 3 || dil.size() != 3)
+            throw invalid(OP, "pad must have 6 elements, stride and dilation 3");
+        for (int32_t p : pad)
+            if (p < 0)
+                throw invalid(OP, "pad must be non-negative");
+        for (int32_t sv : stride)
+            if (sv < 1)
+                throw invalid(OP, "stride must be at least 1");
+        for (int32_t dv : dil)
+            if (dv < 1)
+                throw invalid(OP, "dilation must be at least 1");
+        const int64_t ic = input->shape[4];
+        if (weight->shape[4] != ic)
+            throw Error(ERR_SHAPE_MISMATCH, OP + ": weight input channels " + std::to_string(weight->shape[4]) +
+                                                " != input channels " + std::to_string(ic));
+        const int64_t od = output_extent(OP, input->shape[1], pad[0], pad[1], weight->shape[1], dil[0], stride[0]);
+        const int64_t oh = output_extent(OP, input->shape[2], pad[2], pad[3], weight->shape[2], dil[1], stride[1]);
+        const int64_t ow = output_extent(OP, input->shape[3], pad[4], pad[5], weight->shape[3], dil[2], stride[2]);
+        d.n = int32_t(input->shape[0]);
+        d.id = int32_t(input->shape[1]);
+        d.ih = int32_t(input->shape[2]);
+        d.iw = int32_t(input->shape[3]);
+        d.c = int32_t(ic);
+        d.oc = int32_t(weight->shape[0]);
+        d.kd = int32_t(weight->shape[1]);
+        d.kh = int32_t(weight->shape[2]);
+        d.kw = int32_t(weight->shape[3]);
+        d.od = int32_t(od);
+        d.oh = int32_t(oh);
+        d.ow = int32_t(ow);
+        d.pf = pad[0];
+        d.pt = pad[2];
+        d.pl = pad[4];
+        d.sz = stride[0];
+        d.sy = stride[1];
+        d.sx = stride[2];
+        d.dz = dil[0];
+        d.dy = dil[1];
+        d.dx = dil[2];
+        out_shape = {input->shape[0], od, oh, ow, weight->shape[0]};
+    }
+    const int64_t oc = out_shape.back();
+    const int64_t bc = bias->shape[0];
+    if (bc != oc && bc != 1)
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": bias channels " + std::to_string(bc) +
+                                            " must be 1 or match output channels " + std::to_string(oc));
+    const DType in_t = input->dtype(), w_t = weight->dtype(), out_t = bias->dtype(), acc_t = op.attr.acc_type;
+    auto declared = check_declared_output(st, OP, op.outputs[0], out_shape);
+    if (declared && *declared != out_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": output dtype " + dtype_name(*declared) + " does not match bias dtype " +
+                                            dtype_name(out_t));
+    if (!standard_types(in_t, w_t, acc_t, out_t))
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": unsupported types input=" + dtype_name(in_t) + " weight=" +
+                                            dtype_name(w_t) + " acc=" + dtype_name(acc_t) + " output=" +
+                                            dtype_name(out_t));
+    if (in_zp->dtype() != in_t || w_zp->dtype() != w_t)
+        throw Error(ERR_DTYPE_MISMATCH, OP + ": zero points must match input/weight dtypes");
+    const bool is_int = dtype_is_int(acc_t);
+    if (is_int) {
+        d.zp_x = int_values(*in_zp)[0];
+        d.zp_w = int_values(*w_zp)[0];
+        if (d.zp_x != 0 && in_t != DT_INT8)
+            throw invalid(OP, "input zero point must be zero for non-int8 input");
+        if (d.zp_w != 0 && w_t != DT_INT8)
+            throw invalid(OP, "weight zero point must be zero for non-int8 weight");
+    } else {
+        d.fzp_x = float(float_values(*in_zp)[0]);
+        d.fzp_w = float(float_values(*w_zp)[0]);
+        if (d.fzp_x != 0.0f || d.fzp_w != 0.0f)
+            throw invalid(OP, "zero points must be zero for floating-point operands");
+    }
+    const int64_t count = shape_count(out_shape);
+    if (shape_count(input->shape) >= (int64_t(1) << 31) || count >= (int64_t(1) << 31))
+        throw Error(ERR_SHAPE_MISMATCH, OP + ": tensors of 2^31 elements or more are not supported");
+    d.xe = elem_code(in_t);
+    d.we = elem_code(w_t);
+    d.be = elem_code(out_t);
+    d.oe = elem_code(out_t);
+    d.acc = is_int ? (acc_t == DT_INT32 ? ACC_I32 : ACC_I64) : float_acc(acc_t);
+    d.bias_len = int32_t(bc);
+    d.out_fmt = fmt_code(out_t);
+    auto out = new_output(op.outputs[0], out_shape, out_t);
+    void* od = out->data->device_out();
+    if (count > 0)
+        kern::direct_conv(d, input->data->device_in(), weight->data->device_in(), bias->data->device_in(), od, st.s());
+    st.set(out);
+}
 
 void eval_rescale(ExecState& st, const Operator& op, size_t index)
 {
@@ -1672,8 +2000,13 @@ void dispatch(ExecState& st, const Operator& op, size_t index)
     case OP_TRANSPOSE: eval_transpose(st, op); return;
     case OP_CONV2D: eval_conv(st, op, index, false); return;
     case OP_DEPTHWISE_CONV2D: eval_conv(st, op, index, true); return;
-    case OP_MATMUL: eval_matmul(st, op, index); return;
+    case OP_MATMUL: eval_matmul(st, op, index, false); return;
+    case OP_MATMUL_T: eval_matmul(st, op, index, true); return;
+    case OP_CONV3D: eval_conv_nd(st, op, false); return;
+    case OP_TRANSPOSE_CONV2D: eval_conv_nd(st, op, true); return;
     case OP_AVG_POOL2D: eval_avg_pool2d(st, op); return;
+    case OP_MAX_POOL2D: eval_max_pool2d(st, op); return;
+    case OP_CAST: eval_cast(st, op); return;
     case OP_RESCALE: eval_rescale(st, op, index); return;
     case OP_CLAMP: eval_clamp(st, op); return;
     case OP_ADD: eval_add(st, op, index); return;
