@@ -30,8 +30,9 @@ DTYPES = ["UNKNOWN", "BOOL", "INT4", "INT8", "INT16", "INT32", "INT48", "FP32", 
 DTYPE = {n: i for i, n in enumerate(DTYPES)}
 
 # schema/tosa.fbs:88-191 (subset): operator code == its attribute union tag.
-OPS = {"AVG_POOL2D": 2, "CONV2D": 3, "DEPTHWISE_CONV2D": 5, "MATMUL": 7, "CLAMP": 11, "ADD": 15,
-       "RESHAPE": 57, "TRANSPOSE": 61, "RESCALE": 66, "CONST": 67, "IDENTITY": 68, "CONST_SHAPE": 75}
+OPS = {"AVG_POOL2D": 2, "CONV2D": 3, "CONV3D": 4, "DEPTHWISE_CONV2D": 5, "MATMUL": 7, "MAX_POOL2D": 8,
+       "TRANSPOSE_CONV2D": 10, "CLAMP": 11, "ADD": 15, "RESHAPE": 57, "TRANSPOSE": 61, "CAST": 65, "RESCALE": 66,
+       "CONST": 67, "IDENTITY": 68, "CONST_SHAPE": 75, "MATMUL_T": 100}
 ROUNDING = {"SINGLE_ROUND": 1, "INEXACT_ROUND": 2, "DOUBLE_ROUND": 3}
 NAN_MODE = {"PROPAGATE": 1, "IGNORE": 2}
 
@@ -198,13 +199,22 @@ class GraphBuilder:
     def _attribute(op, a):
         """(union tag, attribute table) with the field order of schema/tosa.fbs:298-520."""
         code = OPS[op]
-        if op in ("CONV2D", "DEPTHWISE_CONV2D"):
+        if op in ("CONV2D", "CONV3D", "DEPTHWISE_CONV2D"):
             return code, _Table([(0, "off", _Vec("i32", a["pad"])), (1, "off", _Vec("i32", a["stride"])),
                                  (2, "off", _Vec("i32", a["dilation"])), (3, "bool", a.get("local_bound", 0)),
                                  (4, "u32", DTYPE[a["acc_type"]])])
         if op == "AVG_POOL2D":
             return code, _Table([(0, "off", _Vec("i32", a["kernel"])), (1, "off", _Vec("i32", a["stride"])),
                                  (2, "off", _Vec("i32", a["pad"])), (3, "u32", DTYPE[a["acc_type"]])])
+        if op == "MAX_POOL2D":
+            return code, _Table([(0, "off", _Vec("i32", a["kernel"])), (1, "off", _Vec("i32", a["stride"])),
+                                 (2, "off", _Vec("i32", a["pad"])),
+                                 (3, "u32", NAN_MODE[a.get("nan_mode", "PROPAGATE")])])
+        if op == "TRANSPOSE_CONV2D":
+            return code, _Table([(0, "off", _Vec("i32", a["out_pad"])), (1, "off", _Vec("i32", a["stride"])),
+                                 (2, "bool", a.get("local_bound", 0)), (3, "u32", DTYPE[a["acc_type"]])])
+        if op == "CAST":
+            return code, _Table([(0, "bool", a.get("input_unsigned", 0))])
         if op == "CLAMP":
             return code, _Table([(0, "off", _Vec("u8", a["min_val"], align=8)),
                                  (1, "off", _Vec("u8", a["max_val"], align=8)),
