@@ -196,3 +196,62 @@ def test_cast_large(pair):
         nan = np.isnan(rv)
         assert np.array_equal(np.isnan(gv), nan)
         assert np.array_equal(O.encode(to, gv)[~nan].view(np.uint8), O.encode(to, rv)[~nan].view(np.uint8))
+
+
+# int16 on the int8 MFMA kernels: each int16 operand split into two int8
+# halves, partial products combined in int64 and clamped to 48 bits.
+@pytest.mark.parametrize("geom", [((2, 14, 14, 64), 64, 3, [1, 1, 1, 1], [1, 1]),
+                                  ((2, 16, 17, 64), 48, 3, [0, 1, 1, 1], [2, 2]),
+                                  ((3, 9, 10, 48), 32, 1, [0, 0, 0, 0], [1, 1])])
+@pytest.mark.parametrize("rescale16", [False, True])
+def test_conv2d_int16_split(geom, rescale16):
+    xs, oc, k, pad, stride = geom
+    r = rng_for("conv_i16", geom)
+    x = r.integers(-2 ** 15, 2 ** 15, xs).astype(np.int16)
+    x.reshape(-1)[:4] = [-2 ** 15, 2 ** 15 - 1, 0, -1]
+    w = r.integers(-128, 128, (oc, k, k, xs[3])).astype(np.int8)
+    bias = r.integers(-2 ** 40, 2 ** 40, oc)
+    oh = (xs[1] + pad[0] + pad[1] - k) // stride[0] + 1
+    ow = (xs[2] + pad[2] + pad[3] - k) // stride[1] + 1
+    g = GraphBuilder()
+    g.input("x", list(xs), "INT16")
+    g.const("w", w, "INT8")
+    g.const("b", bias, "INT48")
+    g.const("zx", np.array([0]), "INT16")
+    g.const("zw", np.array([-7]), "INT8")
+    g.tensor("y", [xs[0], oh, ow, oc], "INT48")
+    g.op("CONV2D", ["x", "w", "b", "zx", "zw"], ["y"], pad=pad, stride=stride, dilation=[1, 1], acc_type="INT48")
+    out = "y"
+    if rescale16:
+        # INT48 -> INT16 through apply_scale_16, per channel, as an int16 network requantises
+        g.const("m", r.integers(2 ** 14, 2 ** 15, oc).astype(np.int16), "INT16")
+        g.const("s", r.integers(34, 40, oc).astype(np.int8), "INT8")
+        g.const("iz", np.array([0]), "INT48")
+        g.const("oz", np.array([0]), "INT16")
+        g.tensor("q", [xs[0], oh, ow, oc], "INT16")
+        g.op("RESCALE", ["y", "m", "s", "iz", "oz"], ["q"], scale32=0, rounding_mode="SINGLE_ROUND", per_channel=1)
+        out = "q"
+    graph = g.build([out])
+    ins = {"x": (x, "INT16")}
+    assert same(run(graph, ins)[out].numpy(), oracle_run(graph, ins)[out].vals)
+
+
+@pytest.mark.parametrize("kind,d", [("MATMUL", 2), ("MATMUL_T", 2), ("MATMUL_T", 1)])
+def test_matmul_int16_split(kind, d):
+    n, h, c, w = 2, 64, 128, 96
+    r = rng_for("mm_i16", kind, d)
+    a = r.integers(-2 ** 15, 2 ** 15, (n, h, c)).astype(np.int16)
+    bshape = (n, c, w) if kind == "MATMUL" else (d, w, c)
+    b = r.integers(-2 ** 15, 2 ** 15, bshape).astype(np.int16)
+    a.reshape(-1)[:c] = -2 ** 15   # a row of extremes against B's first column
+    b.reshape(-1)[:2] = [-2 ** 15, 2 ** 15 - 1]
+    g = GraphBuilder()
+    g.input("a", [n, h, c], "INT16")
+    g.input("b", list(bshape), "INT16")
+    g.const("az", np.array([0]), "INT16")
+    g.const("bz", np.array([0]), "INT16")
+    g.tensor("y", [n, h, w], "INT48")
+    g.op(kind, ["a", "b", "az", "bz"], ["y"])
+    graph = g.build(["y"])
+    ins = {"a": (a, "INT16"), "b": (b, "INT16")}
+    assert same(run(graph, ins)["y"].numpy(), oracle_run(graph, ins)["y"].vals)

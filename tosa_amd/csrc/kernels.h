@@ -315,6 +315,13 @@ struct CastDesc {
 };
 void cast(const CastDesc& d, const void* x, int64_t count, void* out, hipStream_t stream);
 
+// int16 x as int8 halves: x = 256 hi + (lo + 128), hi = x >> 8.
+void split_i16(const int16_t* x, int64_t count, int8_t* hi, int8_t* lo, hipStream_t stream);
+// out[i] = clamp48(sum_k coef[k] parts[k][i] + bias), int64 arithmetic;
+// bias (INT48 as int64) per channel i % channels, or one value, or null.
+void combine_i48(const int32_t* const* parts, const int64_t* coef, int nparts, const int64_t* bias, int32_t bias_len,
+                 int32_t channels, int64_t count, int64_t* out, hipStream_t stream);
+
 // Standalone RESCALE over `count` elements of element code `xe`.
 void rescale(const RescaleDev& rs, ElemCode xe, const void* x, int64_t count, void* out, uint32_t* err,
              hipStream_t stream);

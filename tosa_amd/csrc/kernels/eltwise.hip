@@ -1,5 +1,6 @@
-// Bandwidth-bound kernels: int8 DEPTHWISE_CONV2D, AVG_POOL2D, RESCALE,
-// CLAMP, ADD, the fused quantised residual add, and TRANSPOSE.
+// Bandwidth-bound kernels: int8 DEPTHWISE_CONV2D, AVG_POOL2D, MAX_POOL2D,
+// RESCALE, CAST, CLAMP, ADD, the fused quantised residual add, TRANSPOSE,
+// and the int16 split / INT48 assembly around the int8 MFMA kernels.
 #include "kcommon.h"
 
 #pragma clang fp contract(off)
@@ -571,6 +572,47 @@ __global__ void cast_kernel(CastDesc d, const void* x, int64_t count, void* out)
     }
 }
 
+
+// int16 values as two int8 halves for the int8 MFMA kernels: x = 256 hi +
+// lo with hi = x >> 8 (arithmetic) and lo = x & 255, stored as lo - 128 so
+// that it fits int8 (a kernel input zero point of -128 gives lo back).
+__global__ void split_i16_kernel(const int16_t* x, int64_t count, int8_t* hi, int8_t* lo)
+{
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= count)
+        return;
+    const int32_t v = x[i];
+    hi[i] = int8_t(v >> 8);
+    lo[i] = int8_t((v & 255) - 128);
+}
+
+// INT48 result of products of int16 operands assembled from int32 partial
+// sums of their int8 halves: out = clamp48(sum_k coef[k] part[k] + bias),
+// in int64 (the reference's AccI64 and its final clamp, src/ops/conv.rs:
+// 465-473, src/ops/matmul.rs:150-153).
+struct I48Parts {
+    const int32_t* part[4];
+    int64_t coef[4];
+    int32_t nparts;
+    const int64_t* bias;  // [bias_len] or null
+    int32_t bias_len;
+    int32_t channels;     // bias index = i % channels when bias_len > 1
+};
+
+__global__ void combine_i48_kernel(I48Parts p, int64_t count, int64_t* out)
+{
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= count)
+        return;
+    int64_t v = 0;
+    for (int k = 0; k < p.nparts; k++)
+        v += p.coef[k] * int64_t(p.part[k][i]);
+    if (p.bias)
+        v += p.bias[p.bias_len == 1 ? 0 : i % p.channels];
+    const int64_t lo = -(int64_t(1) << 47), hi = (int64_t(1) << 47) - 1;
+    out[i] = v < lo ? lo : (v > hi ? hi : v);
+}
+
 }  // namespace
 
 // The residual kernel without per-element checks applies when every REQUIRE
@@ -637,6 +679,28 @@ void avg_pool2d(const PoolDesc& d, const void* x, void* out, uint32_t* err, hipS
     } else {
         hipLaunchKernelGGL(avg_pool_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, d, x, out, err, total);
     }
+}
+
+void split_i16(const int16_t* x, int64_t count, int8_t* hi, int8_t* lo, hipStream_t stream)
+{
+    if (count > 0)
+        hipLaunchKernelGGL(split_i16_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, x, count, hi, lo);
+}
+
+void combine_i48(const int32_t* const* parts, const int64_t* coef, int nparts, const int64_t* bias, int32_t bias_len,
+                 int32_t channels, int64_t count, int64_t* out, hipStream_t stream)
+{
+    I48Parts p{};
+    p.nparts = nparts;
+    for (int k = 0; k < nparts; k++) {
+        p.part[k] = parts[k];
+        p.coef[k] = coef[k];
+    }
+    p.bias = bias;
+    p.bias_len = bias_len;
+    p.channels = channels;
+    if (count > 0)
+        hipLaunchKernelGGL(combine_i48_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, p, count, out);
 }
 
 void max_pool2d(const PoolDesc& d, bool ignore, float lowest, const void* x, void* out, hipStream_t stream)

@@ -1108,6 +1108,66 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
         return;
     }
 
+    // int16 x int8 -> INT48 (src/ops/conv.rs:457-473, AccI64) on the int8
+    // MFMA kernels. The input as int8 halves, x = 256 hi + lo with lo held as
+    // lo - 128: the sum of x (w - zw) is 256 times that of hi plus that of
+    // (lo - 128) - (-128), i.e. a second convolution with input zero point
+    // -128 (which padding taps also take, so they still add nothing). Each
+    // half accumulates in int32 without wrapping while K 255 255 < 2^31; the
+    // two combine with the bias in int64, clamped to 48 bits.
+    if (is_int && in_t == DT_INT16 && w_t == DT_INT8 && acc_t == DT_INT48 && !depthwise && izp == 0 &&
+        K * 65025 < (int64_t(1) << 31) && sizes_ok() && count > 0) {
+        const int64_t xcount = g.n * g.ih * g.iw * g.ic;
+        auto hi = make_device_storage(DT_INT8, xcount);
+        auto lo = make_device_storage(DT_INT8, xcount);
+        ConvI8Desc fd;
+        fd.x = static_cast<const int8_t*>(hi->device_out());
+        fd.w = static_cast<const int8_t*>(weight->data->device_in());
+        fd.bias = nullptr;
+        fd.bias_len = 1;
+        fd.n = int32_t(g.n);
+        fd.ih = int32_t(g.ih);
+        fd.iw = int32_t(g.iw);
+        fd.ic = int32_t(g.ic);
+        fd.oc = int32_t(g.oc);
+        fd.kh = int32_t(g.kh);
+        fd.kw = int32_t(g.kw);
+        fd.oh = int32_t(g.oh);
+        fd.ow = int32_t(g.ow);
+        fd.pt = int32_t(g.pt);
+        fd.pl = int32_t(g.pl);
+        fd.sy = int32_t(g.sy);
+        fd.sx = int32_t(g.sx);
+        fd.dy = int32_t(g.dy);
+        fd.dx = int32_t(g.dx);
+        fd.zp_w = int32_t(wzp);
+        if (conv_i8_fast_supported(fd)) {
+            hipStream_t s = st.s();
+            const bool w_const = st.is_const(op.inputs[1]);
+            kern::split_i16(static_cast<const int16_t*>(input->data->device_in()), xcount,
+                            static_cast<int8_t*>(hi->device_out()), static_cast<int8_t*>(lo->device_out()), s);
+            auto wp = conv_i8_wpack_for(fd, *weight->data, w_const, s);
+            fd.wpack = wp ? static_cast<const int8_t*>(wp->device_in()) : nullptr;
+            ConvI8Desc dl = fd;
+            dl.x = static_cast<const int8_t*>(lo->device_in());
+            dl.zp_x = -128;
+            auto th = conv_i8_table_for(fd, *weight->data, nullptr, nullptr, w_const, s);
+            auto tl = conv_i8_table_for(dl, *weight->data, nullptr, nullptr, w_const, s);
+            auto ph = make_device_storage(DT_INT32, count);
+            auto pl = make_device_storage(DT_INT32, count);
+            conv_i8_fast(fd, th->device_in(), nullptr, ph->device_out(), st.err(), s);
+            conv_i8_fast(dl, tl->device_in(), nullptr, pl->device_out(), st.err(), s);
+            auto out = new_output(out_name, g.out_shape, DT_INT48);
+            const int32_t* parts[2] = {static_cast<const int32_t*>(ph->device_in()),
+                                       static_cast<const int32_t*>(pl->device_in())};
+            const int64_t coef[2] = {256, 1};
+            kern::combine_i48(parts, coef, 2, static_cast<const int64_t*>(bias->data->device_in()), int32_t(bc),
+                              int32_t(g.oc), count, static_cast<int64_t*>(out->data->device_out()), s);
+            st.set(out);
+            return;
+        }
+    }
+
     // Reference-order kernel for every other combination.
     DirectConvDesc d{};
     d.depthwise = depthwise;
@@ -1355,6 +1415,62 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index, bool transpose
         void* od = out->data->device_out();
         if (count > 0)
             kern::gemm(gd, ad, bd, od, st.err(), st.s());
+        st.set(out);
+        return;
+    }
+    // int16 x int16 -> INT48 (src/ops/matmul.rs:147-153) on the int8 MFMA
+    // kernel: both operands as int8 halves (a = 256 ah + al, b = 256 bh + bl,
+    // the lows held minus 128): four int8 products, a low half entering with
+    // zero point -128, combined in int64 as 65536 P(hh) + 256 (P(hl) + P(lh))
+    // + P(ll) and clamped to 48 bits. Exact while C 255 255 < 2^31.
+    if (is_int && a_t == DT_INT16 && out_t == DT_INT48 && small && count > 0 && c % 16 == 0 &&
+        c * 65025 < (int64_t(1) << 31)) {
+        hipStream_t s = st.s();
+        const int64_t acount = n * h * c, bcount = shape_count(b->shape);
+        auto ah = make_device_storage(DT_INT8, acount), al = make_device_storage(DT_INT8, acount);
+        auto bh = make_device_storage(DT_INT8, bcount), bl = make_device_storage(DT_INT8, bcount);
+        kern::split_i16(static_cast<const int16_t*>(a->data->device_in()), acount,
+                        static_cast<int8_t*>(ah->device_out()), static_cast<int8_t*>(al->device_out()), s);
+        kern::split_i16(static_cast<const int16_t*>(b->data->device_in()), bcount,
+                        static_cast<int8_t*>(bh->device_out()), static_cast<int8_t*>(bl->device_out()), s);
+        // B halves as rows of c bytes: MATMUL_T's own layout, MATMUL's transposed.
+        auto rows = [&](const StoragePtr& half) {
+            if (transposed)
+                return half;
+            auto t = make_device_storage(DT_INT8, bcount);
+            transpose_b_i8(static_cast<const int8_t*>(half->device_in()), int32_t(n), int32_t(c), int32_t(w),
+                           static_cast<int8_t*>(t->device_out()), s);
+            return t;
+        };
+        const StoragePtr bhr = rows(bh), blr = rows(bl);
+        ConvI8Desc fd;
+        fd.bias = nullptr;
+        fd.bias_len = 1;
+        fd.n = 1;
+        fd.ih = fd.oh = int32_t(broadcast ? n * h : h);
+        fd.iw = fd.ow = 1;
+        fd.ic = int32_t(c);
+        fd.oc = int32_t(w);
+        fd.batch = int32_t(broadcast ? 1 : n);
+        auto part = [&](const StoragePtr& x8, const StoragePtr& w8, int32_t zx, int32_t zw) {
+            ConvI8Desc d = fd;
+            d.x = static_cast<const int8_t*>(x8->device_in());
+            d.w = static_cast<const int8_t*>(w8->device_in());
+            d.zp_x = zx;
+            d.zp_w = zw;
+            auto tab = conv_i8_table_for(d, *w8, nullptr, nullptr, false, s);
+            auto out = make_device_storage(DT_INT32, count);
+            conv_i8_fast(d, tab->device_in(), nullptr, out->device_out(), st.err(), s);
+            return out;
+        };
+        const StoragePtr p[4] = {part(ah, bhr, 0, 0), part(ah, blr, 0, -128), part(al, bhr, -128, 0),
+                                 part(al, blr, -128, -128)};
+        auto out = new_output(out_name, out_shape, DT_INT48);
+        const int32_t* parts[4];
+        for (int k = 0; k < 4; k++)
+            parts[k] = static_cast<const int32_t*>(p[k]->device_in());
+        const int64_t coef[4] = {65536, 256, 256, 1};
+        kern::combine_i48(parts, coef, 4, nullptr, 1, 1, count, static_cast<int64_t*>(out->data->device_out()), s);
         st.set(out);
         return;
     }
