@@ -5,6 +5,7 @@
 
 #include "../../include/tosa_mi355x.h"
 #include "interpreter.h"
+#include "kernels.h"
 #include "opapi.h"
 
 using namespace tosa;
@@ -558,6 +559,8 @@ tosa_status tosa_set_option(const char* key, int value)
         o.strict_float = value != 0;
     else if (std::strcmp(key, "deferred") == 0)
         o.deferred = value != 0;
+    else if (std::strcmp(key, "conv_rows") == 0)
+        kern::set_conv_rows_enabled(value != 0);
     else
         return fail(TOSA_ERR_INVALID_ARGUMENT, std::string("unknown option ") + key);
     return TOSA_OK;
@@ -574,6 +577,8 @@ int tosa_get_option(const char* key)
         return o.strict_float;
     if (std::strcmp(key, "deferred") == 0)
         return o.deferred;
+    if (std::strcmp(key, "conv_rows") == 0)
+        return kern::conv_rows_enabled();
     return -1;
 }
 

@@ -151,6 +151,10 @@ void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t
 void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream);
 // Compute units of the current device.
 int cu_count();
+// Whether int8 3x3 convolutions that fit it run on the row-tile kernel
+// (default) rather than the halo kernel; both are bit-exact.
+void set_conv_rows_enabled(bool on);
+bool conv_rows_enabled();
 // 1x1 stride-1 int8 CONV2D with the fused RESCALE to int8 on the streaming
 // pointwise kernel, for the shapes it takes (conv_i8.hip: K <= 64 a multiple
 // of 8, many pixels); false otherwise.

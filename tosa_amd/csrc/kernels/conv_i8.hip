@@ -27,6 +27,7 @@
 // lane ends up holding 4*TM consecutive output channels of one pixel, which
 // the epilogue stores as one vector.
 #include <algorithm>
+#include <atomic>
 
 #include <stdexcept>
 #include <type_traits>
@@ -1295,6 +1296,311 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 }
 
 // ---------------------------------------------------------------------------
+// Row-tile int8 3x3 convolution: stride 1, no dilation, output rows of 17 to
+// 32 pixels, 128 input channels, no weight zero point (the ResNet-scale
+// [N,28,28,128] layers). A workgroup of four waves (one per SIMD) computes
+// 32 CB output channels x RG RW output rows, each wave 32 channels x RW
+// rows: one 32-pixel MFMA tile per output row, output pixel ox in lane ox
+// (lanes past the row read the row's last pixel and store nothing).
+//
+// For reduction chunk q (32 input channels) and column tap kx, the B
+// fragment of halo row hr is the operand of row tap ky for output row
+// hr - ky: one LDS read feeds up to three MFMAs, where raster-order pixel
+// tiles need one read per MFMA. The wave's A fragments (the whole
+// reduction: IC / 32 x 9 of them) stay in VGPRs, loaded once from the
+// packed weights (32-channel blocks), each workgroup starting at its own
+// chunk. The halo (HR rows x HW positions x IC bytes; 16-byte chunk c of
+// position pos stored at chunk c ^ ((pos >> 1) & 7), so that 16
+// consecutive positions reading one chunk hit 16 distinct bank groups) is
+// one LDS image, loaded through VGPRs, padding from the zero-point fill.
+// The rows run in phases; each phase's epilogue is issued between the next
+// phase's MFMAs (a wave overlaps its own VALU work with its matrix work
+// while it issues fewer than about four VALU instructions per MFMA).
+// ---------------------------------------------------------------------------
+struct RowsArgs {
+    const int8_t* x;
+    const int8_t* wp;  // packed weights, 32-channel blocks
+    const v4i* tab;    // [N][2] entries, 16 bytes of the input zero point, [N] additive constants
+    const int8_t* zfill;
+    int32_t N, IC, IH, IW, OH, OW, pt, pl;
+    int32_t HW;         // halo positions per row (OW + 2)
+    int32_t row_tiles;  // per image
+    int32_t ch_tiles;   // 32 CB channels each
+    int32_t hbytes;     // LDS bytes of the halo image (1 KB multiple)
+    FastDiv div_hw;
+    EpiArgs E;
+};
+
+constexpr int ROWS_RW = 7;  // output rows per wave
+
+template <int Q, int CB, int OB, bool RS, bool RC>
+__global__ void __launch_bounds__(256, 1) conv_i8_rows_kernel(RowsArgs A)
+{
+    static_assert(Q == 4, "128 input channels");
+    static_assert(CB == 2 || CB == 4, "64 or 128 channels per workgroup");
+    static_assert(!RC || RS, "the range check belongs to the RESCALE");
+    constexpr int RW = ROWS_RW;
+    constexpr int RG = 4 / CB;  // waves along the rows
+    constexpr int PB = 32 * Q;  // halo bytes per position
+    constexpr int SL = 2 * Q;   // 16-byte chunks per position
+    constexpr int S = 3 * Q;    // (q, kx) steps of a phase
+
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t* const halo = smem;
+    v4i* const s_tab = reinterpret_cast<v4i*>(smem + A.hbytes);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cb = wave % CB, rg = wave / CB;
+    const int l32 = lane & 31;
+    const int h = lane >> 5;
+    // Tile t of XCD x is workgroup x + 8 t (workgroups are dealt round-robin
+    // to the XCDs), so that the channel tiles and neighbouring row tiles of
+    // an image, which read the same input rows, meet in one L2.
+    const int tile = (gridDim.x & 7) == 0 ? (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int rt = tile / A.ch_tiles;
+    const int ct = tile - rt * A.ch_tiles;
+    const int img = rt / A.row_tiles;
+    const int oy0 = (rt - img * A.row_tiles) * (RG * RW);
+    const int n0 = ct * 32 * CB;
+    const int nw = n0 + 32 * cb;  // the wave's first channel
+    const int rowb = A.HW * PB;
+    const int HR = RG * RW + 2;
+    static_assert(((RG * RW + 2) * 34 * SL + 255) / 256 <= 32, "halo slots per lane");
+
+    // Accumulator start values: the additive constants of this lane's
+    // channels nw + 16 h + i.
+    v16i init;
+    {
+        const v4i* adds =
+            reinterpret_cast<const v4i*>(reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1) + nw + 16 * h);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const v4i v = adds[k];
+            init[4 * k] = v.x;
+            init[4 * k + 1] = v.y;
+            init[4 * k + 2] = v.z;
+            init[4 * k + 3] = v.w;
+        }
+    }
+    // Register slot q holds reduction chunk (q + rot) % Q: the sums do not
+    // depend on the order, and workgroups that start at different chunks
+    // spread their simultaneous weight requests over more L2 lines.
+    const int rot = tile & (Q - 1);
+    auto chunk = [&](int q) { return (q + rot) & (Q - 1); };
+    // The wave's A fragments: chunk c, tap t at ((block Q + c) 9 + t) KB.
+    const int8_t* const wsrc = A.wp + int64_t(nw >> 5) * (Q * 9 * 1024) + lane * 16;
+    v4i aw[Q][9];
+#pragma unroll
+    for (int t = 0; t < 9; t++)
+        aw[0][t] = *reinterpret_cast<const v4i*>(wsrc + (chunk(0) * 9 + t) * 1024);
+
+    // Table entries of the workgroup's channels and the halo image: 16-byte
+    // loads into VGPRs (they issue several times faster than direct
+    // global->LDS loads), written to LDS once they land. Lane l of wave w
+    // takes halo slot s = 256 i + 64 w + l; slots past the image load the
+    // zero-point fill into the padding.
+    constexpr int NI = ((RG * RW + 2) * 34 * SL + 255) / 256;  // slots per lane at the widest rows
+    const int total = HR * A.HW * SL;
+    v4i hv[NI];
+    {
+        const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.IC;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int sl = 256 * i + 64 * wave + lane;
+            if (256 * i + 64 * wave < total) {
+                const int hp = sl / SL;
+                const int hr = fdiv(hp, A.div_hw);
+                const int pos = hp - hr * A.HW;
+                const int c = (sl & (SL - 1)) ^ ((pos >> 1) & (SL - 1));
+                const int iy = oy0 - A.pt + hr;
+                const int ix = pos - A.pl;
+                const bool ok = sl < total && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
+                hv[i] = *reinterpret_cast<const v4i*>(ok ? xi + (int64_t(iy) * A.IW + ix) * A.IC + 16 * c : A.zfill);
+            }
+        }
+    }
+    v4i tv = v4i{0, 0, 0, 0};
+    if (wave < CB)
+        tv = A.tab[2 * n0 + tid];
+#pragma unroll
+    for (int q = 1; q < Q; q++)
+#pragma unroll
+        for (int t = 0; t < 9; t++)
+            aw[q][t] = *reinterpret_cast<const v4i*>(wsrc + (chunk(q) * 9 + t) * 1024);
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        if (256 * i + 64 * wave < total)
+            *reinterpret_cast<v4i*>(halo + (256 * i + 64 * wave + lane) * 16) = hv[i];
+    if (wave < CB)
+        s_tab[tid] = tv;
+    __syncthreads();
+
+    // Per-lane byte offsets of the B fragments within a halo row.
+    int boff[3][Q];
+    {
+        const int ox = l32 < A.OW ? l32 : A.OW - 1;
+#pragma unroll
+        for (int kx = 0; kx < 3; kx++) {
+            const int pos = ox + kx;
+#pragma unroll
+            for (int q = 0; q < Q; q++)
+                boff[kx][q] = pos * PB + (((2 * chunk(q) + h) ^ ((pos >> 1) & (SL - 1))) << 4);
+        }
+    }
+    const uint8_t* const hb = halo + rg * RW * rowb;
+
+    v16i acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+        acc[r] = init;
+
+    // Epilogue: in units of 4 values (channel group g of row b); a group's
+    // table entries are read one group ahead. res[b]: the row's 16 results,
+    // OB bytes each.
+    uint32_t bad_bits = 0;
+    uint32_t res[RW][4 * OB];
+    v4i t0[4], t1[4];
+    auto tab_load = [&](int g, v4i(&u0)[4], v4i(&u1)[4]) {
+        const int cl = 32 * cb + 16 * h + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            u0[i] = s_tab[2 * (cl + i)];
+            if constexpr (RS)
+                u1[i] = s_tab[2 * (cl + i) + 1];
+        }
+    };
+    auto unit = [&](int b, int g) {
+        int32_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int32_t x = acc[b][4 * g + i];
+            if constexpr (RS) {
+                // apply_scale_32 with the per-sign rounding constant (the
+                // output zero point folded in), then the output range and
+                // CLAMP; with RC, its value-range REQUIRE.
+                if constexpr (RC)
+                    bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(x, t0[i].z, ~t0[i].z)),
+                                                           uint32_t(x), 0xf6);  // bad | (med3 ^ x)
+                const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
+                const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
+                const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
+                v[i] = med3(r, A.E.clo, A.E.chi);
+            } else {
+                v[i] = x;
+            }
+        }
+        if constexpr (OB == 1) {
+            // Low bytes of v0..v3 (v_perm_b32: selector bytes 0-3 pick the
+            // second operand, 4-7 the first, 0x0c zero).
+            const uint32_t p01 = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x0c0c0400u);
+            const uint32_t p23 = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x0c0c0400u);
+            res[b][g] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+        } else if constexpr (OB == 2) {
+            res[b][2 * g] = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u);
+            res[b][2 * g + 1] = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                res[b][4 * g + i] = uint32_t(v[i]);
+        }
+    };
+    auto store = [&](int b) {
+        const int oy = oy0 + rg * RW + b;
+        if (oy < A.OH && l32 < A.OW) {
+            const int64_t m = (int64_t(img) * A.OH + oy) * A.OW + l32;
+            uint8_t* const dst = A.E.out + (m * A.N + nw + 16 * h) * OB;
+#pragma unroll
+            for (int wd = 0; wd < OB; wd++)
+                *reinterpret_cast<v4u*>(dst + 16 * wd) =
+                    v4u{res[b][4 * wd], res[b][4 * wd + 1], res[b][4 * wd + 2], res[b][4 * wd + 3]};
+        }
+    };
+
+    // The rows run in phases of 2, 2, 2 and 1 rows. The epilogue of a
+    // phase's rows (units of 4 values: channel group g of row b, groups
+    // outer, a group's table entries read at its first unit) runs between the
+    // next phase's MFMAs, the last phase's after them. Step s = (q, kx) of a
+    // phase reads the next step's P + 2 B fragments, issues its 3 P MFMAs
+    // and its share of the previous phase's units; scheduling groups then
+    // place one MFMA, at most one LDS read and NV VALU instructions in turn
+    // (a wave issues one instruction at a time, and a run of other
+    // instructions longer than an MFMA's 32 cycles leaves the matrix pipe
+    // idle).
+    auto epi_units = [&](int e0, int ep, int u0, int u1) {
+#pragma unroll
+        for (int u = u0; u < u1; u++) {
+            const int g = u / ep, b = e0 + u - ep * (u / ep);
+            if (b == e0)
+                tab_load(g, t0, t1);
+            unit(b, g);
+        }
+    };
+    auto phase = [&](auto r0c, auto pc, auto e0c, auto epc) {
+        constexpr int R0 = decltype(r0c)::value, P = decltype(pc)::value;
+        constexpr int E0 = decltype(e0c)::value, EP = decltype(epc)::value;  // EP 0: no epilogue
+        constexpr int U = 4 * EP;
+        constexpr int NM = 3 * P, ND = P + 2;
+        // VALU per MFMA: the units' share (about 32 instructions a unit)
+        // and one address add per read.
+        constexpr int NV = (U * 32 / S + ND + NM - 1) / NM;
+        v4i bf[2][P + 2];
+        auto ldb = [&](v4i(&bb)[P + 2], int st) {
+            const int q = st / 3, kx = st - 3 * (st / 3);
+#pragma unroll
+            for (int j = 0; j < P + 2; j++)
+                bb[j] = *reinterpret_cast<const v4i*>(hb + (R0 + j) * rowb + boff[kx][q]);
+        };
+        ldb(bf[0], 0);
+#pragma unroll
+        for (int st = 0; st < S; st++) {
+            const int q = st / 3, kx = st - 3 * (st / 3);
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + 1 < S)
+                ldb(bf[(st + 1) & 1], st + 1);
+#pragma unroll
+            for (int ky = 0; ky < 3; ky++)
+#pragma unroll
+                for (int r = 0; r < P; r++)
+                    acc[R0 + r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[q][3 * ky + kx], bf[st & 1][r + ky],
+                                                                        acc[R0 + r], 0, 0, 0);
+            if constexpr (EP > 0)
+                epi_units(E0, EP, st * U / S, (st + 1) * U / S);
+#pragma unroll
+            for (int i = 0; i < NM; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU (a read's address first)
+                if (i < ND && st + 1 < S)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EP > 0) {
+#pragma unroll
+            for (int r = E0; r < E0 + EP; r++)
+                store(r);
+        }
+    };
+    using std::integral_constant;
+    static_assert(RW == 7, "phases of 2, 2, 2 and 1 rows");
+    phase(integral_constant<int, 0>{}, integral_constant<int, 2>{}, integral_constant<int, 0>{},
+          integral_constant<int, 0>{});
+    phase(integral_constant<int, 2>{}, integral_constant<int, 2>{}, integral_constant<int, 0>{},
+          integral_constant<int, 2>{});
+    phase(integral_constant<int, 4>{}, integral_constant<int, 2>{}, integral_constant<int, 2>{},
+          integral_constant<int, 2>{});
+    phase(integral_constant<int, 6>{}, integral_constant<int, 1>{}, integral_constant<int, 4>{},
+          integral_constant<int, 2>{});
+    epi_units(6, 1, 0, 4);
+    store(6);
+    if constexpr (RC) {
+        if (bad_bits)
+            atomicOr(A.E.err, DERR_SCALE_RANGE);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Streaming pointwise int8 convolution for short reductions (1x1, stride 1,
 // K <= 64): a layer that moves K bytes in and N bytes out per pixel is
 // memory-bound, and the tiled kernels' per-workgroup staging and barriers
@@ -2319,6 +2625,13 @@ void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob,
 
 }  // namespace
 
+namespace {
+std::atomic<int> g_conv_rows{1};
+}  // namespace
+
+void set_conv_rows_enabled(bool on) { g_conv_rows.store(on ? 1 : 0); }
+bool conv_rows_enabled() { return g_conv_rows.load() != 0; }
+
 // Compute units of the current device (workgroups of the 32x32 halo kernel
 // that run at once: its LDS allows one per CU).
 int cu_count()
@@ -2437,6 +2750,72 @@ bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& l
     lds = lds_for(R, bc, h32_bp(PG, TB), a.KP);
     blocks = unsigned(d.n) * unsigned(a.tiles_per_img);
     return true;
+}
+
+// Geometry of the row-tile kernel for `d`, or false when it does not apply:
+// a 3x3 stride-1 undilated CONV2D with 128 input channels, output rows of
+// 17-32 pixels, output channels a multiple of 64 and no weight zero point
+// (one workgroup per CU). CB: 32-channel
+// blocks per workgroup (4 when the channels allow, else 2 and two waves
+// along the rows).
+bool rows_plan(const ConvI8Desc& d, RowsArgs& a, int& cb, size_t& lds, unsigned& blocks)
+{
+    if (!conv_rows_enabled() || d.depthwise || d.kh != 3 || d.kw != 3 || d.sy != 1 || d.sx != 1 || d.dy != 1 ||
+        d.dx != 1 || d.zp_w != 0 || d.ic != 128 || d.ow < 17 || d.ow > 32 || d.oc % 64 != 0 || d.batch != 1)
+        return false;
+    cb = d.oc % 128 == 0 ? 4 : 2;
+    const int rg = 4 / cb;
+    const int rows = rg * ROWS_RW;
+    a.x = d.x;
+    a.wp = d.wpack;
+    a.N = d.oc;
+    a.IC = d.ic;
+    a.IH = d.ih;
+    a.IW = d.iw;
+    a.OH = d.oh;
+    a.OW = d.ow;
+    a.pt = d.pt;
+    a.pl = d.pl;
+    a.HW = d.ow + 2;
+    a.row_tiles = (d.oh + rows - 1) / rows;
+    a.ch_tiles = d.oc / (32 * cb);
+    a.hbytes = int32_t((int64_t(rows + 2) * a.HW * d.ic + 1023) / 1024 * 1024);
+    a.div_hw = FastDiv(uint32_t(a.HW));
+    lds = size_t(a.hbytes) + size_t(cb) * 32 * 2 * 16;
+    const int64_t nb = int64_t(d.n) * a.row_tiles * a.ch_tiles;
+    if (nb >= (int64_t(1) << 31))
+        return false;
+    blocks = unsigned(nb);
+    return true;
+}
+
+template <int CB, int OB, bool RS, bool RC>
+void launch_rows(const RowsArgs& a, unsigned blocks, size_t lds, hipStream_t s)
+{
+    auto kfn = conv_i8_rows_kernel<4, CB, OB, RS, RC>;
+    static bool attr = [&]() {
+        hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      HALO_LDS_MAX),
+                  "conv_i8 rows LDS size");
+        return true;
+    }();
+    (void)attr;
+    if (lds > size_t(HALO_LDS_MAX))
+        throw std::runtime_error("conv_i8 rows: LDS image too large");
+    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(256), lds, s, a);
+}
+
+template <int CB>
+void launch_rows_epi(const RowsArgs& a, unsigned blocks, size_t lds, int ob, bool rs, bool rc, hipStream_t s)
+{
+    if (!rs)
+        launch_rows<CB, 4, false, false>(a, blocks, lds, s);
+    else if (ob == 1)
+        rc ? launch_rows<CB, 1, true, true>(a, blocks, lds, s) : launch_rows<CB, 1, true, false>(a, blocks, lds, s);
+    else if (ob == 2)
+        rc ? launch_rows<CB, 2, true, true>(a, blocks, lds, s) : launch_rows<CB, 2, true, false>(a, blocks, lds, s);
+    else
+        rc ? launch_rows<CB, 4, true, true>(a, blocks, lds, s) : launch_rows<CB, 4, true, false>(a, blocks, lds, s);
 }
 
 template <int G, int OB, bool RS, bool ZW>
@@ -2693,7 +3072,13 @@ int conv_i8_wpack_block(const ConvI8Desc& d)
     unsigned blocks = 0;
     const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
                     d.iw == d.ow;
-    if (pw || !conv_i8_fast_supported(d) || !halo32_plan(d, d.zp_w != 0, a, bc, lds, blocks))
+    if (pw || !conv_i8_fast_supported(d))
+        return 0;
+    RowsArgs ra{};
+    int cb = 0;
+    if (rows_plan(d, ra, cb, lds, blocks))
+        return 32;
+    if (!halo32_plan(d, d.zp_w != 0, a, bc, lds, blocks))
         return 0;
     return bc;
 }
@@ -2813,6 +3198,18 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     int bc = 128, kc = 128;
     size_t lds = 0;
     unsigned blocks = 0;
+    RowsArgs ra{};
+    int cb = 0;
+    if (!pw && d.wpack && rows_plan(d, ra, cb, lds, blocks)) {
+        ra.tab = static_cast<const v4i*>(tab);
+        ra.zfill = reinterpret_cast<const int8_t*>(ra.tab + 2 * d.oc);
+        ra.E = e;
+        if (cb == 4)
+            launch_rows_epi<4>(ra, blocks, lds, ob, rs != nullptr, e.range != 0, stream);
+        else
+            launch_rows_epi<2>(ra, blocks, lds, ob, rs != nullptr, e.range != 0, stream);
+        return;
+    }
     Halo32Args h32{};
     if (!pw && d.wpack && halo32_plan(d, zw, h32, bc, lds, blocks)) {
         h32.tab = static_cast<const v4i*>(tab);
