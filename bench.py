@@ -57,7 +57,7 @@ def parse():
 
 
 HEADLINE = "conv_rescale_64x28x28x128"
-HEADLINE_KERNEL = "conv_i8_halo32_kernel"
+HEADLINE_KERNEL = "conv_i8_rows_kernel"
 # name -> (builder name in tosa_amd.workloads, kwargs, count ops, steps override)
 WORKLOADS = {
     HEADLINE: ("conv_rescale", dict(n=64, h=28, w=28, cin=128, cout=128), True, None),

@@ -168,7 +168,7 @@ tosa_status tosa_run_graph_with_hooks(const uint8_t* data, size_t len, tosa_tens
  * value-dependent REQUIRE failures (RESCALE range/overflow) of such runs are
  * reported by the next tosa_synchronize. Validation errors are unaffected.
  * "conv_rows" (default 1, process-wide): int8 3x3 stride-1 CONV2D with 128
- * input channels and 17-32 pixel output rows runs on the row-tile kernel;
+ * input channels and 17-30 pixel output rows runs on the row-tile kernel;
  * 0 selects the halo kernel. Both are bit-exact. */
 tosa_status tosa_set_option(const char* key, int value);
 int tosa_get_option(const char* key);

@@ -2,10 +2,12 @@
 tosa_amd/csrc/kernels/conv_i8.hip) against the oracle, bit for bit.
 
 The kernel takes 3x3 stride-1 CONV2D with 128 input channels, output rows of
-17-32 pixels and output channels a multiple of 64. The cases pick what its
+17-30 pixels and output channels a multiple of 64; producer waves issue the
+MFMAs and hand each phase's accumulators through LDS to consumer waves that
+run the epilogue. The cases pick what its
 indexing depends on: 128-channel workgroups (CB 4) and 64-channel ones with
 two waves along the rows (CB 2, also with three channel tiles); row counts
-that leave the last row tile partial; the narrowest (17) and widest (32)
+that leave the last row tile partial; the narrowest (17) and widest (30)
 rows; asymmetric and zero padding (halo positions from the zero-point fill);
 int32 output (the fused epilogue's pass-through, and the unfused graph),
 RESCALE to int8 and int16 with per-channel and per-tensor SINGLE/DOUBLE
@@ -28,7 +30,7 @@ ROWS = [
     # n, h, w, oc, pad
     (2, 28, 28, 128, (1, 1, 1, 1)),
     (1, 20, 20, 64, (1, 1, 1, 1)),
-    (3, 30, 32, 192, (1, 1, 1, 1)),
+    (3, 30, 30, 192, (1, 1, 1, 1)),
     (1, 19, 19, 128, (0, 0, 0, 0)),
     (2, 16, 26, 256, (1, 0, 2, 1)),
     (1, 9, 30, 320, (1, 1, 1, 1)),

@@ -1297,25 +1297,32 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 
 // ---------------------------------------------------------------------------
 // Row-tile int8 3x3 convolution: stride 1, no dilation, output rows of 17 to
-// 32 pixels, 128 input channels, no weight zero point (the ResNet-scale
-// [N,28,28,128] layers). A workgroup of four waves (one per SIMD) computes
-// 32 CB output channels x RG RW output rows, each wave 32 channels x RW
-// rows: one 32-pixel MFMA tile per output row, output pixel ox in lane ox
-// (lanes past the row read the row's last pixel and store nothing).
+// 30 pixels, 128 input channels, no weight zero point (the ResNet-scale
+// [N,28,28,128] layers). A workgroup computes 32 CB output channels x RG RW
+// output rows with eight waves, two per SIMD: four producer waves issue the
+// MFMAs and four consumer waves run the epilogue, so that the epilogue's
+// VALU work issues beside the other wave's matrix work instead of between
+// its own MFMAs.
 //
-// For reduction chunk q (32 input channels) and column tap kx, the B
-// fragment of halo row hr is the operand of row tap ky for output row
-// hr - ky: one LDS read feeds up to three MFMAs, where raster-order pixel
-// tiles need one read per MFMA. The wave's A fragments (the whole
-// reduction: IC / 32 x 9 of them) stay in VGPRs, loaded once from the
-// packed weights (32-channel blocks), each workgroup starting at its own
-// chunk. The halo (HR rows x HW positions x IC bytes; 16-byte chunk c of
-// position pos stored at chunk c ^ ((pos >> 1) & 7), so that 16
-// consecutive positions reading one chunk hit 16 distinct bank groups) is
-// one LDS image, loaded through VGPRs, padding from the zero-point fill.
-// The rows run in phases; each phase's epilogue is issued between the next
-// phase's MFMAs (a wave overlaps its own VALU work with its matrix work
-// while it issues fewer than about four VALU instructions per MFMA).
+// Producer wave p owns 32 channels x RW rows: one 32-pixel MFMA tile per
+// output row, output pixel ox in lane ox (lanes past the row compute the
+// padded positions and store nothing). For reduction chunk q (32 input
+// channels) and column tap kx, the B fragment of halo row hr is the operand
+// of row tap ky for output row hr - ky: one LDS read feeds up to three
+// MFMAs. The wave's A fragments (the whole reduction: IC / 32 x 9 of them)
+// stay in VGPRs, loaded once from the packed weights, each workgroup
+// starting at its own chunk; the accumulators start at the channels'
+// additive constants. Rows run in phases of 2, 2, 2 and 1; at the end of a
+// phase the producer writes its accumulators to a transfer buffer in LDS
+// (two buffers, alternating) and the workgroup meets at a barrier; the
+// consumer wave p + 4 then turns those rows into output bytes (RESCALE,
+// CLAMP, packing, stores) while its producer computes the next phase.
+//
+// The halo (HR rows x 32 positions x IC bytes; 16-byte chunk c of position
+// pos stored at chunk c ^ ((pos >> 1) & 7), so that 16 consecutive
+// positions reading one chunk hit 16 distinct bank groups) is one LDS image
+// loaded by all eight waves, positions outside the image from the
+// zero-point fill; the consumers stage the epilogue table through LDS.
 // ---------------------------------------------------------------------------
 struct RowsArgs {
     const int8_t* x;
@@ -1323,36 +1330,51 @@ struct RowsArgs {
     const v4i* tab;    // [N][2] entries, 16 bytes of the input zero point, [N] additive constants
     const int8_t* zfill;
     int32_t N, IC, IH, IW, OH, OW, pt, pl;
-    int32_t HW;         // halo positions per row (OW + 2)
     int32_t row_tiles;  // per image
     int32_t ch_tiles;   // 32 CB channels each
-    int32_t hbytes;     // LDS bytes of the halo image (1 KB multiple)
-    FastDiv div_hw;
     EpiArgs E;
 };
 
-constexpr int ROWS_RW = 7;  // output rows per wave
+constexpr int ROWS_RW = 7;    // output rows per producer wave
+constexpr int ROWS_HWP = 32;  // halo positions per row (output rows of at most 30 pixels)
+
+// LDS bytes of the row-tile kernel: halo image, two transfer buffers of
+// two rows per producer wave, epilogue table.
+constexpr size_t rows_lds(int cb)
+{
+    return size_t(4 / cb * ROWS_RW + 2) * ROWS_HWP * 128 + 2 * 4 * 2 * 4096 + size_t(cb) * 32 * 2 * 16;
+}
 
 template <int Q, int CB, int OB, bool RS, bool RC>
-__global__ void __launch_bounds__(256, 1) conv_i8_rows_kernel(RowsArgs A)
+__global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
 {
     static_assert(Q == 4, "128 input channels");
     static_assert(CB == 2 || CB == 4, "64 or 128 channels per workgroup");
     static_assert(!RC || RS, "the range check belongs to the RESCALE");
     constexpr int RW = ROWS_RW;
-    constexpr int RG = 4 / CB;  // waves along the rows
+    constexpr int RG = 4 / CB;  // producer waves along the rows
     constexpr int PB = 32 * Q;  // halo bytes per position
     constexpr int SL = 2 * Q;   // 16-byte chunks per position
-    constexpr int S = 3 * Q;    // (q, kx) steps of a phase
+    constexpr int HWP = ROWS_HWP;
+    constexpr int HR = RG * RW + 2;
+    constexpr int SLOTS = HR * HWP * SL;  // 16-byte halo slots
+    constexpr int NI = (SLOTS + 511) / 512;
+    constexpr int HBYTES = SLOTS * 16;
+    constexpr int ROWB = HWP * PB;
+    constexpr int XW = 2 * 4096;  // transfer bytes per producer wave and buffer (two rows)
+    constexpr int XB = 4 * XW;    // transfer bytes per buffer
+    static_assert(rows_lds(CB) == size_t(HBYTES + 2 * XB + 2 * 32 * CB * 16), "LDS layout");
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* const halo = smem;
-    v4i* const s_tab = reinterpret_cast<v4i*>(smem + A.hbytes);
+    uint8_t* const xfer = smem + HBYTES;  // [2][4 waves][2 rows][4 chunks][64 lanes][16 B]
+    v4i* const s_tab = reinterpret_cast<v4i*>(smem + HBYTES + 2 * XB);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int cb = wave % CB, rg = wave / CB;
+    const int pw = wave & 3;  // the producer wave (consumer wave pw + 4 serves it)
+    const int cb = pw % CB, rg = pw / CB;
     const int l32 = lane & 31;
     const int h = lane >> 5;
     // Tile t of XCD x is workgroup x + 8 t (workgroups are dealt round-robin
@@ -1364,240 +1386,242 @@ __global__ void __launch_bounds__(256, 1) conv_i8_rows_kernel(RowsArgs A)
     const int img = rt / A.row_tiles;
     const int oy0 = (rt - img * A.row_tiles) * (RG * RW);
     const int n0 = ct * 32 * CB;
-    const int nw = n0 + 32 * cb;  // the wave's first channel
-    const int rowb = A.HW * PB;
-    const int HR = RG * RW + 2;
-    static_assert(((RG * RW + 2) * 34 * SL + 255) / 256 <= 32, "halo slots per lane");
-
-    // Accumulator start values: the additive constants of this lane's
-    // channels nw + 16 h + i.
-    v16i init;
-    {
-        const v4i* adds =
-            reinterpret_cast<const v4i*>(reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1) + nw + 16 * h);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const v4i v = adds[k];
-            init[4 * k] = v.x;
-            init[4 * k + 1] = v.y;
-            init[4 * k + 2] = v.z;
-            init[4 * k + 3] = v.w;
-        }
-    }
+    const int nw = n0 + 32 * cb;  // the producer's first channel
     // Register slot q holds reduction chunk (q + rot) % Q: the sums do not
     // depend on the order, and workgroups that start at different chunks
     // spread their simultaneous weight requests over more L2 lines.
     const int rot = tile & (Q - 1);
     auto chunk = [&](int q) { return (q + rot) & (Q - 1); };
-    // The wave's A fragments: chunk c, tap t at ((block Q + c) 9 + t) KB.
-    const int8_t* const wsrc = A.wp + int64_t(nw >> 5) * (Q * 9 * 1024) + lane * 16;
-    v4i aw[Q][9];
-#pragma unroll
-    for (int t = 0; t < 9; t++)
-        aw[0][t] = *reinterpret_cast<const v4i*>(wsrc + (chunk(0) * 9 + t) * 1024);
 
-    // Table entries of the workgroup's channels and the halo image: 16-byte
-    // loads into VGPRs (they issue several times faster than direct
-    // global->LDS loads), written to LDS once they land. Lane l of wave w
-    // takes halo slot s = 256 i + 64 w + l; slots past the image load the
-    // zero-point fill into the padding.
-    constexpr int NI = ((RG * RW + 2) * 34 * SL + 255) / 256;  // slots per lane at the widest rows
-    const int total = HR * A.HW * SL;
+    // Halo slot s = 512 i + tid: chunk s % SL of position (s / SL) % HWP of
+    // halo row s / (SL HWP).
     v4i hv[NI];
-    {
+    auto halo_load = [&]() {
         const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.IC;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int sl = 256 * i + 64 * wave + lane;
-            if (256 * i + 64 * wave < total) {
+            const int sl = 512 * i + tid;
+            if (512 * i + 64 * wave < SLOTS) {
                 const int hp = sl / SL;
-                const int hr = fdiv(hp, A.div_hw);
-                const int pos = hp - hr * A.HW;
-                const int c = (sl & (SL - 1)) ^ ((pos >> 1) & (SL - 1));
+                const int hr = hp / HWP;
+                const int pos = hp % HWP;
+                const int c = (sl % SL) ^ ((pos >> 1) % SL);
                 const int iy = oy0 - A.pt + hr;
                 const int ix = pos - A.pl;
-                const bool ok = sl < total && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
+                const bool ok = hr < HR && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
                 hv[i] = *reinterpret_cast<const v4i*>(ok ? xi + (int64_t(iy) * A.IW + ix) * A.IC + 16 * c : A.zfill);
             }
         }
-    }
-    v4i tv = v4i{0, 0, 0, 0};
-    if (wave < CB)
-        tv = A.tab[2 * n0 + tid];
+    };
+    auto halo_store = [&]() {
 #pragma unroll
-    for (int q = 1; q < Q; q++)
-#pragma unroll
-        for (int t = 0; t < 9; t++)
-            aw[q][t] = *reinterpret_cast<const v4i*>(wsrc + (chunk(q) * 9 + t) * 1024);
-#pragma unroll
-    for (int i = 0; i < NI; i++)
-        if (256 * i + 64 * wave < total)
-            *reinterpret_cast<v4i*>(halo + (256 * i + 64 * wave + lane) * 16) = hv[i];
-    if (wave < CB)
-        s_tab[tid] = tv;
-    __syncthreads();
+        for (int i = 0; i < NI; i++)
+            if (512 * i + 64 * wave < SLOTS && 512 * i + tid < SLOTS)
+                *reinterpret_cast<v4i*>(halo + (512 * i + tid) * 16) = hv[i];
+    };
 
-    // Per-lane byte offsets of the B fragments within a halo row.
-    int boff[3][Q];
-    {
-        const int ox = l32 < A.OW ? l32 : A.OW - 1;
+    using std::integral_constant;
+    using I0 = integral_constant<int, 0>;
+    using I1 = integral_constant<int, 1>;
+    using I2 = integral_constant<int, 2>;
+    using I4 = integral_constant<int, 4>;
+    using I6 = integral_constant<int, 6>;
+    static_assert(RW == 7, "phases of 2, 2, 2 and 1 rows");
+
+    auto producer = [&]() {
+        halo_load();
+        v4i aw[Q][9];  // chunk q, tap t at ((block Q + chunk(q)) 9 + t) KB
+        {
+            const int8_t* const wsrc = A.wp + int64_t(nw >> 5) * (Q * 9 * 1024) + lane * 16;
+#pragma unroll
+            for (int q = 0; q < Q; q++)
+#pragma unroll
+                for (int t = 0; t < 9; t++)
+                    aw[q][t] = *reinterpret_cast<const v4i*>(wsrc + (chunk(q) * 9 + t) * 1024);
+        }
+        v16i init;  // the additive constants of this lane's channels nw + 16 h + i
+        {
+            const v4i* adds =
+                reinterpret_cast<const v4i*>(reinterpret_cast<const int32_t*>(A.tab + 2 * A.N + 1) + nw + 16 * h);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const v4i v = adds[k];
+                init[4 * k] = v.x;
+                init[4 * k + 1] = v.y;
+                init[4 * k + 2] = v.z;
+                init[4 * k + 3] = v.w;
+            }
+        }
+        halo_store();
+        __syncthreads();
+
+        // Byte offsets of this lane's B fragments within a halo row: position
+        // l32 + kx (clamped to the row; such lanes are past the output row),
+        // chunk 2 q + h.
+        int boff[3][Q];
 #pragma unroll
         for (int kx = 0; kx < 3; kx++) {
-            const int pos = ox + kx;
+            const int pos = l32 + kx < HWP ? l32 + kx : HWP - 1;
 #pragma unroll
             for (int q = 0; q < Q; q++)
                 boff[kx][q] = pos * PB + (((2 * chunk(q) + h) ^ ((pos >> 1) & (SL - 1))) << 4);
         }
-    }
-    const uint8_t* const hb = halo + rg * RW * rowb;
+        const uint8_t* const hb = halo + rg * RW * ROWB;
 
-    v16i acc[RW];
+        // Rows R0 .. R0 + P - 1: step s = (q, kx) reads the next step's P + 2
+        // B fragments and issues its 3 P MFMAs; the accumulators go to
+        // transfer buffer BUF.
+        auto phase = [&](auto r0c, auto pc, auto bufc) {
+            constexpr int R0 = decltype(r0c)::value, P = decltype(pc)::value, BUF = decltype(bufc)::value;
+            constexpr int S = 3 * Q, NM = 3 * P, ND = P + 2;
+            v16i acc[P];
 #pragma unroll
-    for (int r = 0; r < RW; r++)
-        acc[r] = init;
-
-    // Epilogue: in units of 4 values (channel group g of row b); a group's
-    // table entries are read one group ahead. res[b]: the row's 16 results,
-    // OB bytes each.
-    uint32_t bad_bits = 0;
-    uint32_t res[RW][4 * OB];
-    v4i t0[4], t1[4];
-    auto tab_load = [&](int g, v4i(&u0)[4], v4i(&u1)[4]) {
-        const int cl = 32 * cb + 16 * h + 4 * g;
+            for (int r = 0; r < P; r++)
+                acc[r] = init;
+            v4i bf[2][ND];
+            auto ldb = [&](v4i(&bb)[ND], int st) {
+                const int q = st / 3, kx = st - 3 * (st / 3);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            u0[i] = s_tab[2 * (cl + i)];
-            if constexpr (RS)
-                u1[i] = s_tab[2 * (cl + i) + 1];
-        }
-    };
-    auto unit = [&](int b, int g) {
-        int32_t v[4];
+                for (int j = 0; j < ND; j++)
+                    bb[j] = *reinterpret_cast<const v4i*>(hb + (R0 + j) * ROWB + boff[kx][q]);
+            };
+            ldb(bf[0], 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int32_t x = acc[b][4 * g + i];
-            if constexpr (RS) {
-                // apply_scale_32 with the per-sign rounding constant (the
-                // output zero point folded in), then the output range and
-                // CLAMP; with RC, its value-range REQUIRE.
-                if constexpr (RC)
-                    bad_bits = __builtin_amdgcn_bitop3_b32(bad_bits, uint32_t(med3(x, t0[i].z, ~t0[i].z)),
-                                                           uint32_t(x), 0xf6);  // bad | (med3 ^ x)
-                const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[i].x, t1[i].y});
-                const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[i].z, t1[i].w});
-                const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
-                v[i] = med3(r, A.E.clo, A.E.chi);
-            } else {
-                v[i] = x;
+            for (int st = 0; st < S; st++) {
+                const int q = st / 3, kx = st - 3 * (st / 3);
+                __builtin_amdgcn_sched_barrier(0);
+                if (st + 1 < S)
+                    ldb(bf[(st + 1) & 1], st + 1);
+#pragma unroll
+                for (int ky = 0; ky < 3; ky++)
+#pragma unroll
+                    for (int r = 0; r < P; r++)
+                        acc[r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[q][3 * ky + kx], bf[st & 1][r + ky], acc[r],
+                                                                       0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < NM; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    if (i < ND && st + 1 < S)
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+                }
             }
-        }
-        if constexpr (OB == 1) {
-            // Low bytes of v0..v3 (v_perm_b32: selector bytes 0-3 pick the
-            // second operand, 4-7 the first, 0x0c zero).
-            const uint32_t p01 = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x0c0c0400u);
-            const uint32_t p23 = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x0c0c0400u);
-            res[b][g] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
-        } else if constexpr (OB == 2) {
-            res[b][2 * g] = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u);
-            res[b][2 * g + 1] = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                res[b][4 * g + i] = uint32_t(v[i]);
-        }
-    };
-    auto store = [&](int b) {
-        const int oy = oy0 + rg * RW + b;
-        if (oy < A.OH && l32 < A.OW) {
-            const int64_t m = (int64_t(img) * A.OH + oy) * A.OW + l32;
-            uint8_t* const dst = A.E.out + (m * A.N + nw + 16 * h) * OB;
-#pragma unroll
-            for (int wd = 0; wd < OB; wd++)
-                *reinterpret_cast<v4u*>(dst + 16 * wd) =
-                    v4u{res[b][4 * wd], res[b][4 * wd + 1], res[b][4 * wd + 2], res[b][4 * wd + 3]};
-        }
-    };
-
-    // The rows run in phases of 2, 2, 2 and 1 rows. The epilogue of a
-    // phase's rows (units of 4 values: channel group g of row b, groups
-    // outer, a group's table entries read at its first unit) runs between the
-    // next phase's MFMAs, the last phase's after them. Step s = (q, kx) of a
-    // phase reads the next step's P + 2 B fragments, issues its 3 P MFMAs
-    // and its share of the previous phase's units; scheduling groups then
-    // place one MFMA, at most one LDS read and NV VALU instructions in turn
-    // (a wave issues one instruction at a time, and a run of other
-    // instructions longer than an MFMA's 32 cycles leaves the matrix pipe
-    // idle).
-    auto epi_units = [&](int e0, int ep, int u0, int u1) {
-#pragma unroll
-        for (int u = u0; u < u1; u++) {
-            const int g = u / ep, b = e0 + u - ep * (u / ep);
-            if (b == e0)
-                tab_load(g, t0, t1);
-            unit(b, g);
-        }
-    };
-    auto phase = [&](auto r0c, auto pc, auto e0c, auto epc) {
-        constexpr int R0 = decltype(r0c)::value, P = decltype(pc)::value;
-        constexpr int E0 = decltype(e0c)::value, EP = decltype(epc)::value;  // EP 0: no epilogue
-        constexpr int U = 4 * EP;
-        constexpr int NM = 3 * P, ND = P + 2;
-        // VALU per MFMA: the units' share (about 32 instructions a unit)
-        // and one address add per read.
-        constexpr int NV = (U * 32 / S + ND + NM - 1) / NM;
-        v4i bf[2][P + 2];
-        auto ldb = [&](v4i(&bb)[P + 2], int st) {
-            const int q = st / 3, kx = st - 3 * (st / 3);
-#pragma unroll
-            for (int j = 0; j < P + 2; j++)
-                bb[j] = *reinterpret_cast<const v4i*>(hb + (R0 + j) * rowb + boff[kx][q]);
-        };
-        ldb(bf[0], 0);
-#pragma unroll
-        for (int st = 0; st < S; st++) {
-            const int q = st / 3, kx = st - 3 * (st / 3);
             __builtin_amdgcn_sched_barrier(0);
-            if (st + 1 < S)
-                ldb(bf[(st + 1) & 1], st + 1);
+            // Lane-contiguous 16-byte pieces: value group k of row r of lane l
+            // at ((r 4 + k) 64 + l) 16.
+            uint8_t* const xb = xfer + BUF * XB + pw * XW;
 #pragma unroll
-            for (int ky = 0; ky < 3; ky++)
+            for (int r = 0; r < P; r++)
 #pragma unroll
-                for (int r = 0; r < P; r++)
-                    acc[R0 + r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[q][3 * ky + kx], bf[st & 1][r + ky],
-                                                                        acc[R0 + r], 0, 0, 0);
-            if constexpr (EP > 0)
-                epi_units(E0, EP, st * U / S, (st + 1) * U / S);
+                for (int k = 0; k < 4; k++)
+                    *reinterpret_cast<v4i*>(xb + ((r * 4 + k) * 64 + lane) * 16) =
+                        v4i{acc[r][4 * k], acc[r][4 * k + 1], acc[r][4 * k + 2], acc[r][4 * k + 3]};
+        };
+        phase(I0{}, I2{}, I0{});
+        __syncthreads();
+        phase(I2{}, I2{}, I1{});
+        __syncthreads();
+        phase(I4{}, I2{}, I0{});
+        __syncthreads();
+        phase(I6{}, I1{}, I1{});
+        __syncthreads();
+    };
+
+    auto consumer = [&]() {
+        halo_load();
+        const int ctid = tid - 256;
+        v4i tv = v4i{0, 0, 0, 0};
+        if (ctid < 2 * 32 * CB)
+            tv = A.tab[2 * n0 + ctid];
+        halo_store();
+        if (ctid < 2 * 32 * CB)
+            s_tab[ctid] = tv;
+        __syncthreads();
+        // Table entries of this lane's channels nw + 16 h + j.
+        v4i t0[16], t1[16];
 #pragma unroll
-            for (int i = 0; i < NM; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU (a read's address first)
-                if (i < ND && st + 1 < S)
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            }
+        for (int j = 0; j < 16; j++) {
+            t0[j] = s_tab[2 * (32 * cb + 16 * h + j)];
+            if constexpr (RS)
+                t1[j] = s_tab[2 * (32 * cb + 16 * h + j) + 1];
         }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (EP > 0) {
+        uint32_t bad_bits = 0;
+        auto finish = [&](auto r0c, auto pc, auto bufc) {
+            constexpr int R0 = decltype(r0c)::value, P = decltype(pc)::value, BUF = decltype(bufc)::value;
+            const uint8_t* const xb = xfer + BUF * XB + pw * XW;
 #pragma unroll
-            for (int r = E0; r < E0 + EP; r++)
-                store(r);
+            for (int r = 0; r < P; r++) {
+                v4i xv[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    xv[k] = *reinterpret_cast<const v4i*>(xb + ((r * 4 + k) * 64 + lane) * 16);
+                uint32_t res[4 * OB];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    int32_t v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int j = 4 * g + i;
+                        const int32_t x = xv[g][i];
+                        if constexpr (RS) {
+                            // apply_scale_32 with the per-sign rounding constant
+                            // (the output zero point folded in), then the output
+                            // range and CLAMP; with RC, its value-range REQUIRE.
+                            if constexpr (RC)
+                                bad_bits = __builtin_amdgcn_bitop3_b32(
+                                    bad_bits, uint32_t(med3(x, t0[j].z, ~t0[j].z)), uint32_t(x), 0xf6);
+                            const int64_t rp = __builtin_bit_cast(int64_t, v2i{t1[j].x, t1[j].y});
+                            const int64_t rn = __builtin_bit_cast(int64_t, v2i{t1[j].z, t1[j].w});
+                            const int32_t rr =
+                                int32_t((int64_t(x) * int64_t(t0[j].y) + (x >= 0 ? rp : rn)) >> t0[j].w);
+                            v[i] = med3(rr, A.E.clo, A.E.chi);
+                        } else {
+                            v[i] = x;
+                        }
+                    }
+                    if constexpr (OB == 1) {
+                        // Low bytes of v0..v3 (v_perm_b32: selector bytes 0-3
+                        // pick the second operand, 4-7 the first, 0x0c zero).
+                        const uint32_t p01 = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x0c0c0400u);
+                        const uint32_t p23 = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x0c0c0400u);
+                        res[g] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+                    } else if constexpr (OB == 2) {
+                        res[2 * g] = __builtin_amdgcn_perm(uint32_t(v[1]), uint32_t(v[0]), 0x05040100u);
+                        res[2 * g + 1] = __builtin_amdgcn_perm(uint32_t(v[3]), uint32_t(v[2]), 0x05040100u);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            res[4 * g + i] = uint32_t(v[i]);
+                    }
+                }
+                const int oy = oy0 + rg * RW + R0 + r;
+                if (oy < A.OH && l32 < A.OW) {
+                    const int64_t m = (int64_t(img) * A.OH + oy) * A.OW + l32;
+                    uint8_t* const dst = A.E.out + (m * A.N + nw + 16 * h) * OB;
+#pragma unroll
+                    for (int wd = 0; wd < OB; wd++)
+                        *reinterpret_cast<v4u*>(dst + 16 * wd) =
+                            v4u{res[4 * wd], res[4 * wd + 1], res[4 * wd + 2], res[4 * wd + 3]};
+                }
+            }
+        };
+        __syncthreads();
+        finish(I0{}, I2{}, I0{});
+        __syncthreads();
+        finish(I2{}, I2{}, I1{});
+        __syncthreads();
+        finish(I4{}, I2{}, I0{});
+        __syncthreads();
+        finish(I6{}, I1{}, I1{});
+        if constexpr (RC) {
+            if (bad_bits)
+                atomicOr(A.E.err, DERR_SCALE_RANGE);
         }
     };
-    using std::integral_constant;
-    static_assert(RW == 7, "phases of 2, 2, 2 and 1 rows");
-    phase(integral_constant<int, 0>{}, integral_constant<int, 2>{}, integral_constant<int, 0>{},
-          integral_constant<int, 0>{});
-    phase(integral_constant<int, 2>{}, integral_constant<int, 2>{}, integral_constant<int, 0>{},
-          integral_constant<int, 2>{});
-    phase(integral_constant<int, 4>{}, integral_constant<int, 2>{}, integral_constant<int, 2>{},
-          integral_constant<int, 2>{});
-    phase(integral_constant<int, 6>{}, integral_constant<int, 1>{}, integral_constant<int, 4>{},
-          integral_constant<int, 2>{});
-    epi_units(6, 1, 0, 4);
-    store(6);
-    if constexpr (RC) {
-        if (bad_bits)
-            atomicOr(A.E.err, DERR_SCALE_RANGE);
-    }
+    // Both roles meet at the same five barriers.
+    if (wave < 4)
+        producer();
+    else
+        consumer();
 }
 
 // ---------------------------------------------------------------------------
@@ -2754,18 +2778,17 @@ bool halo32_plan(const ConvI8Desc& d, bool zw, Halo32Args& a, int& bc, size_t& l
 
 // Geometry of the row-tile kernel for `d`, or false when it does not apply:
 // a 3x3 stride-1 undilated CONV2D with 128 input channels, output rows of
-// 17-32 pixels, output channels a multiple of 64 and no weight zero point
-// (one workgroup per CU). CB: 32-channel
-// blocks per workgroup (4 when the channels allow, else 2 and two waves
-// along the rows).
+// 17-30 pixels, output channels a multiple of 64 and no weight zero point
+// (one workgroup per CU). CB: 32-channel blocks per workgroup (4 when the
+// channels allow, else 2 and two producer waves along the rows).
 bool rows_plan(const ConvI8Desc& d, RowsArgs& a, int& cb, size_t& lds, unsigned& blocks)
 {
     if (!conv_rows_enabled() || d.depthwise || d.kh != 3 || d.kw != 3 || d.sy != 1 || d.sx != 1 || d.dy != 1 ||
-        d.dx != 1 || d.zp_w != 0 || d.ic != 128 || d.ow < 17 || d.ow > 32 || d.oc % 64 != 0 || d.batch != 1)
+        d.dx != 1 || d.zp_w != 0 || d.ic != 128 || d.ow < 17 || d.ow > ROWS_HWP - 2 || d.oc % 64 != 0 ||
+        d.batch != 1)
         return false;
     cb = d.oc % 128 == 0 ? 4 : 2;
-    const int rg = 4 / cb;
-    const int rows = rg * ROWS_RW;
+    const int rows = 4 / cb * ROWS_RW;
     a.x = d.x;
     a.wp = d.wpack;
     a.N = d.oc;
@@ -2776,12 +2799,9 @@ bool rows_plan(const ConvI8Desc& d, RowsArgs& a, int& cb, size_t& lds, unsigned&
     a.OW = d.ow;
     a.pt = d.pt;
     a.pl = d.pl;
-    a.HW = d.ow + 2;
     a.row_tiles = (d.oh + rows - 1) / rows;
     a.ch_tiles = d.oc / (32 * cb);
-    a.hbytes = int32_t((int64_t(rows + 2) * a.HW * d.ic + 1023) / 1024 * 1024);
-    a.div_hw = FastDiv(uint32_t(a.HW));
-    lds = size_t(a.hbytes) + size_t(cb) * 32 * 2 * 16;
+    lds = rows_lds(cb);
     const int64_t nb = int64_t(d.n) * a.row_tiles * a.ch_tiles;
     if (nb >= (int64_t(1) << 31))
         return false;
@@ -2802,7 +2822,7 @@ void launch_rows(const RowsArgs& a, unsigned blocks, size_t lds, hipStream_t s)
     (void)attr;
     if (lds > size_t(HALO_LDS_MAX))
         throw std::runtime_error("conv_i8 rows: LDS image too large");
-    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(kfn, dim3(blocks), dim3(512), lds, s, a);
 }
 
 template <int CB>
