@@ -151,6 +151,15 @@ void conv_i8_rowpad(const int8_t* w, int32_t rows, int32_t k, int32_t kp, int8_t
 void transpose_b_i8(const int8_t* b, int32_t batch, int32_t c, int32_t w, int8_t* out, hipStream_t stream);
 // Compute units of the current device.
 int cu_count();
+// Batched int8 MATMUL a [batch][H][C] x b [batch][C][W] (+ fused RESCALE)
+// in one kernel that reads B in its own layout (matmul_i8_kernel,
+// conv_i8.hip); `tab` is conv_i8_table's output for a descriptor with w null
+// (no weight sums: the kernel adds -zp_a sum_c b itself). Takes C % 128 == 0,
+// W % 16 == 0 and 16-byte aligned operands; false otherwise (nothing done).
+bool matmul_i8_direct_applies(int32_t C, int32_t W, const void* a, const void* b);
+bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H, int32_t C, int32_t W, int32_t zp_a,
+                      int32_t zp_b, const void* tab, const RescaleDev* rs, bool range_safe, void* out, uint32_t* err,
+                      hipStream_t stream);
 // Whether int8 3x3 convolutions that fit it run on the row-tile kernel
 // (default) rather than the halo kernel; both are bit-exact.
 void set_conv_rows_enabled(bool on);

@@ -444,6 +444,219 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args Ain)
 }
 
 // ---------------------------------------------------------------------------
+// Batched int8 MATMUL with B in its own [C][W] layout
+// ---------------------------------------------------------------------------
+// D[h][w] = sum_c (a[h][c] - za)(b[c][w] - zb) for every batch, in one
+// kernel: the B tile of each stage (KC rows of c, 128 columns w) is loaded as
+// 16-byte row pieces and transposed in registers (4 x 4 byte blocks with
+// v_perm_b32) into LDS rows of c bytes per column, the A operand of the same
+// v_mfma_i32_16x16x64_i8 tiling as conv_i8_kernel (columns = its channels,
+// rows of A = its pixels). The zero-point terms come from the staged bytes:
+// -za sum_c b[c][w] (column sums of the transposed dwords, folded into the
+// tile's table entries before the epilogue) and -zb sum_c a[h][c] (row sums,
+// the epilogue's per-pixel term). The table holds the bias-free additive
+// constant K za zb and the RESCALE parameters, independent of B's values.
+// Two register sets keep the loads of two stages ahead in flight; two
+// workgroups share a CU.
+struct MatmulI8Args {
+    const int8_t* a;  // [batch][H][C]
+    const int8_t* b;  // [batch][C][W]
+    const v4i* tab;   // [W][2] entries without column sums
+    int32_t H, C, W;
+    int32_t HT, WT, batch;  // row tiles, column tiles, batches
+    int32_t zp_a;
+    EpiArgs E;  // out [batch][H][W]; E.zp_w is B's zero point
+};
+
+template <int OB, bool RS, bool ZA, bool ZB, bool RC>
+__global__ void __launch_bounds__(256, 2) matmul_i8_kernel(MatmulI8Args A)
+{
+    constexpr int BW = 128, BH = 64, KC = 128;  // columns, rows, K bytes per stage
+    constexpr int WC = 2, WP = 2;
+    constexpr int TM = BW / WC / 16, TN = BH / WP / 16;
+    constexpr int SB = (BW + BH) * KC;  // LDS bytes per stage
+    // 16-byte chunk c of column row `col` of the transposed tile sits at c ^
+    // swzw(col): bits 4-6 of the column, so that the transposing dword writes
+    // (columns 16 apart across lanes) spread over the banks, with bit 1 folded
+    // into bit 2, so that the fragment reads (columns differing in bits 0, 1,
+    // 4, 5 across 16 lanes) hit 16 distinct bank groups.
+    auto swzw = [](int col) { return ((col >> 4) & 7) ^ (((col >> 1) & 1) << 2); };
+
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    v4i* const s_tab = reinterpret_cast<v4i*>(smem + 2 * SB);          // [BW][2]
+    int32_t* const s_rowsum = reinterpret_cast<int32_t*>(s_tab + 2 * BW);  // [BH]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wave_c0 = (wave / WP) * (BW / WC);
+    const int wave_p0 = (wave % WP) * (BH / WP);
+    // Tile t of XCD x is workgroup x + 8 t (workgroups are dealt round-robin
+    // to the XCDs), tiles ordered batch, row tile, column tile: an XCD's
+    // workgroups share whole batches of A and B in its L2.
+    const int ntiles = A.HT * A.WT * A.batch;
+    const int tile = (ntiles & 7) == 0 ? (blockIdx.x & 7) * (ntiles >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int wt = tile % A.WT, ht = (tile / A.WT) % A.HT;
+    const int h0 = ht * BH, w0 = wt * BW;
+    const int64_t bz = tile / (A.WT * A.HT);
+    const int8_t* const a = A.a + bz * A.H * A.C;
+    const int8_t* const b = A.b + bz * A.C * A.W;
+
+    // A: row ra of the tile, 16-byte chunks ca and ca + 4 of each stage;
+    // rows past H re-read row H - 1 (their outputs are not stored).
+    const int ra = tid >> 2, ca = tid & 3;
+    const int8_t* const asrc = a + int64_t(h0 + ra < A.H ? h0 + ra : A.H - 1) * A.C + 16 * ca;
+    // B: rows 4 kg .. 4 kg + 3 of each stage, columns 16 nc .. 16 nc + 15 of
+    // the tile (a last partial tile re-reads the final 16 columns, which land
+    // in columns that are not stored).
+    const int kg = tid >> 3, nc = tid & 7;
+    const int wcol = w0 + 16 * nc + 16 <= A.W ? w0 + 16 * nc : A.W - 16;
+    const int8_t* const bsrc = b + int64_t(4 * kg) * A.W + wcol;
+
+    for (int i = tid; i < 2 * BW; i += 256) {
+        const int c = w0 + (i >> 1);
+        s_tab[i] = A.tab[2 * (c < A.W ? c : A.W - 1) + (i & 1)];
+    }
+
+    v4u av[2][2], bv[2][4];
+    auto load = [&](v4u(&ar)[2], v4u(&br)[4], int k0) {
+        ar[0] = ld16(asrc + k0);
+        ar[1] = ld16(asrc + k0 + 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            br[i] = ld16(bsrc + int64_t(k0 + i) * A.W);
+    };
+    int32_t csum[16];  // column sums of b over this thread's rows (ZA)
+    int32_t rsum = 0;  // row sum of a over this thread's chunks (ZB)
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        csum[i] = 0;
+    auto store = [&](const v4u(&ar)[2], const v4u(&br)[4], int buf) {
+        uint8_t* const sW = smem + buf * SB;
+        uint8_t* const sX = sW + BW * KC;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = ca + 4 * i;
+            *reinterpret_cast<v4u*>(sX + ra * KC + ((c ^ swz<KC>(ra)) << 4)) = ar[i];
+            if constexpr (ZB) {
+                rsum = __builtin_amdgcn_sdot4(int(ar[i].x), 0x01010101, rsum, false);
+                rsum = __builtin_amdgcn_sdot4(int(ar[i].y), 0x01010101, rsum, false);
+                rsum = __builtin_amdgcn_sdot4(int(ar[i].z), 0x01010101, rsum, false);
+                rsum = __builtin_amdgcn_sdot4(int(ar[i].w), 0x01010101, rsum, false);
+            }
+        }
+        // Dword j of the four rows holds columns 4 j .. 4 j + 3; the 4 x 4
+        // byte transpose gives each column its four consecutive k bytes
+        // (v_perm_b32: selector bytes 0-3 pick the second operand, 4-7 the
+        // first).
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t d0 = br[0][j], d1 = br[1][j], d2 = br[2][j], d3 = br[3][j];
+            const uint32_t t0 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);
+            const uint32_t t1 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);
+            const uint32_t t2 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+            const uint32_t t3 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+            const uint32_t e[4] = {__builtin_amdgcn_perm(t2, t0, 0x05040100u), __builtin_amdgcn_perm(t2, t0, 0x07060302u),
+                                   __builtin_amdgcn_perm(t3, t1, 0x05040100u), __builtin_amdgcn_perm(t3, t1, 0x07060302u)};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int col = 16 * nc + 4 * j + m;
+                *reinterpret_cast<uint32_t*>(sW + col * KC + (((kg >> 2) ^ swzw(col)) << 4) + 4 * (kg & 3)) = e[m];
+                if constexpr (ZA)
+                    csum[4 * j + m] = __builtin_amdgcn_sdot4(int(e[m]), 0x01010101, csum[4 * j + m], false);
+            }
+        }
+    };
+
+    v4i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            acc[i][j] = v4i{0, 0, 0, 0};
+    const int j16 = lane & 15;
+    const int grp = lane >> 4;
+    auto compute = [&](int buf) {
+        const uint8_t* const sW = smem + buf * SB;
+        const uint8_t* const sX = sW + BW * KC;
+#pragma unroll
+        for (int ks = 0; ks < KC / 64; ks++) {
+            const int c = ks * 4 + grp;
+            v4i af[TM], bf[TN];
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++) {
+                const int row = wave_c0 + (j16 >> 2) * (4 * TM) + 4 * tm + (j16 & 3);
+                af[tm] = *reinterpret_cast<const v4i*>(sW + row * KC + ((c ^ swzw(row)) << 4));
+            }
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++) {
+                const int row = wave_p0 + 16 * tn + j16;
+                bf[tn] = *reinterpret_cast<const v4i*>(sX + row * KC + ((c ^ swz<KC>(row)) << 4));
+            }
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+                for (int tn = 0; tn < TN; tn++)
+                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+        }
+    };
+
+    // Stage s computes from LDS buffer s % 2; the loads of stage s + 2 are
+    // issued into the register set stage s came from, and stage s + 1's
+    // registers are written to the other buffer before the barrier.
+    const int nst = A.C / KC;
+    load(av[0], bv[0], 0);
+    if (nst > 1)
+        load(av[1], bv[1], KC);
+    store(av[0], bv[0], 0);
+    __syncthreads();
+    for (int s = 0; s < nst; s += 2) {
+        if (s + 2 < nst)
+            load(av[0], bv[0], (s + 2) * KC);
+        compute(0);
+        if (s + 1 < nst)
+            store(av[1], bv[1], 1);
+        __syncthreads();
+        if (s + 1 >= nst)
+            break;
+        if (s + 3 < nst)
+            load(av[1], bv[1], (s + 3) * KC);
+        compute(1);
+        if (s + 2 < nst)
+            store(av[0], bv[0], 0);
+        __syncthreads();
+    }
+
+    // ---- zero-point terms --------------------------------------------------
+    if constexpr (ZA) {
+        // Column sums: 32 row groups x 128 columns, reduced by one thread per
+        // column into its table entry: add -= za sum_c b[c][w].
+        int32_t* const s_cs = reinterpret_cast<int32_t*>(smem);
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            s_cs[kg * BW + 16 * nc + i] = csum[i];
+        __syncthreads();
+        if (tid < BW) {
+            int32_t t = 0;
+            for (int g = 0; g < 32; g++)
+                t += s_cs[g * BW + tid];
+            s_tab[2 * tid].x = int32_t(uint32_t(s_tab[2 * tid].x) - uint32_t(A.zp_a) * uint32_t(t));
+        }
+    }
+    if constexpr (ZB) {
+        rsum += __shfl_xor(rsum, 1);
+        rsum += __shfl_xor(rsum, 2);
+        if (ca == 0)
+            s_rowsum[ra] = rsum;
+    }
+    if constexpr (ZA || ZB)
+        __syncthreads();
+
+    auto pixel = [&](int p) { return h0 + p < A.H ? int(bz * A.H + h0 + p) : -1; };
+    epilogue<TM, TN, OB, RS, ZB, RC>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, w0, wave_p0, j16, A.E, pixel);
+}
+
+// ---------------------------------------------------------------------------
 // Stride-1 convolution over a halo tile
 // ---------------------------------------------------------------------------
 // A workgroup computes BC output channels x R full output rows of one image
@@ -2156,7 +2369,7 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
     // keeps differences, then v_sad_u8), the latter only with a RESCALE.
     int32_t s = 0;
     uint32_t sa = 0;
-    if (zx != 0 || mult) {
+    if (w && (zx != 0 || mult)) {
         const int8_t* wr = w + int64_t(c) * cstride;
         const uint32_t zwb = (uint32_t(uint8_t(zw)) * 0x01010101u) ^ 0x80808080u;
         if (kstride == 1 && K % 16 == 0 && reinterpret_cast<uintptr_t>(wr) % 16 == 0) {
@@ -2206,7 +2419,7 @@ __global__ void conv_i8_table_kernel(const int8_t* w, int32_t N, int32_t K, int3
     // Range bound of apply_scale_32's REQUIRE: values in [lo, ~lo] with
     // lo = -2^min(s - 1, 31).
     int32_t lo = sh - 1 < 31 ? -(int32_t(1) << (sh - 1)) : INT32_MIN;
-    if (mult && lo != INT32_MIN) {
+    if (w && mult && lo != INT32_MIN) {
         const int64_t b = bias ? int64_t(bias[bias_len == 1 ? 0 : c]) : 0;
         const int64_t xmax = std::max<int64_t>(128 + int64_t(zx), 127 - int64_t(zx));
         const uint64_t bound = uint64_t(b < 0 ? -b : b) + sa64 * uint64_t(xmax);
@@ -2871,6 +3084,77 @@ void launch_dw_epi(const DwArgs& a, int ob, bool rs, bool zw, hipStream_t s)
 }
 
 }  // namespace
+
+bool matmul_i8_direct_applies(int32_t C, int32_t W, const void* a, const void* b)
+{
+    return C >= 128 && C % 128 == 0 && W >= 16 && W % 16 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(b) % 16 == 0;
+}
+
+namespace {
+template <int OB, bool RS, bool ZA, bool ZB, bool RC>
+void launch_mm(const MatmulI8Args& a, int32_t batch, hipStream_t s)
+{
+    constexpr size_t lds = 2 * (128 + 64) * 128 + 2 * 128 * 16 + 64 * 4;
+    hipLaunchKernelGGL((matmul_i8_kernel<OB, RS, ZA, ZB, RC>), dim3(unsigned(int64_t(a.HT) * a.WT * batch)), dim3(256),
+                       lds, s, a);
+}
+template <int OB, bool RS, bool RC>
+void launch_mm_zp(const MatmulI8Args& a, int32_t batch, bool za, bool zb, hipStream_t s)
+{
+    if (za)
+        zb ? launch_mm<OB, RS, true, true, RC>(a, batch, s) : launch_mm<OB, RS, true, false, RC>(a, batch, s);
+    else
+        zb ? launch_mm<OB, RS, false, true, RC>(a, batch, s) : launch_mm<OB, RS, false, false, RC>(a, batch, s);
+}
+}  // namespace
+
+bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H, int32_t C, int32_t W, int32_t zp_a,
+                      int32_t zp_b, const void* tab, const RescaleDev* rs, bool range_safe, void* out, uint32_t* err,
+                      hipStream_t stream)
+{
+    if (!matmul_i8_direct_applies(C, W, a, b) || (rs && !conv_i8_fast_epilogue_ok(*rs)))
+        return false;
+    if (int64_t(batch) * H <= 0)
+        return true;
+    MatmulI8Args m{};
+    m.a = a;
+    m.b = b;
+    m.tab = static_cast<const v4i*>(tab);
+    m.H = H;
+    m.C = C;
+    m.W = W;
+    m.HT = (H + 63) / 64;
+    m.WT = (W + 127) / 128;
+    m.batch = batch;
+    if (int64_t(m.HT) * m.WT * batch >= (int64_t(1) << 31))
+        return false;
+    m.zp_a = zp_a;
+    EpiArgs& e = m.E;
+    e.out = static_cast<uint8_t*>(out);
+    e.N = W;
+    e.zp_w = zp_b;
+    e.err = err;
+    int ob = 4;
+    if (rs) {
+        e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
+        e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
+        e.range = rs->min_shift <= 31 && !range_safe;
+        ob = rs->out_bytes;
+    }
+    const bool za = zp_a != 0, zb = zp_b != 0;
+    if (!rs)
+        launch_mm_zp<4, false, false>(m, batch, za, zb, stream);
+    else if (e.range)
+        ob == 1 ? launch_mm_zp<1, true, true>(m, batch, za, zb, stream)
+                : ob == 2 ? launch_mm_zp<2, true, true>(m, batch, za, zb, stream)
+                          : launch_mm_zp<4, true, true>(m, batch, za, zb, stream);
+    else
+        ob == 1 ? launch_mm_zp<1, true, false>(m, batch, za, zb, stream)
+                : ob == 2 ? launch_mm_zp<2, true, false>(m, batch, za, zb, stream)
+                          : launch_mm_zp<4, true, false>(m, batch, za, zb, stream);
+    return true;
+}
 
 bool conv_i8_pointwise_stream(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, void* out, uint32_t* err,
                               hipStream_t stream)

@@ -237,8 +237,8 @@ StoragePtr conv_i8_table_for(const ConvI8Desc& d, Storage& wstore, const void* b
     std::string key;
     if (cacheable) {
         char buf[192];
-        std::snprintf(buf, sizeof buf, "conv_i8_tab:%d:%p:%d:%d:%d:%p:%p:%d:%d:%lld", d.batch, bias_key, d.bias_len,
-                      d.zp_x, d.zp_w, rs ? static_cast<const void*>(rs->mult) : nullptr,
+        std::snprintf(buf, sizeof buf, "conv_i8_tab:%d:%d:%p:%d:%d:%d:%p:%p:%d:%d:%lld", d.w != nullptr, d.batch, bias_key,
+                      d.bias_len, d.zp_x, d.zp_w, rs ? static_cast<const void*>(rs->mult) : nullptr,
                       rs ? static_cast<const void*>(rs->shift) : nullptr, rs ? rs->per_channel : 0,
                       rs ? rs->rounding : 0, rs ? static_cast<long long>(rs->out_zp) : 0LL);
         key = buf;
@@ -1322,6 +1322,19 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index, bool transpose
         auto launch = [fd, a, b, b_const, transposed](void* out, const RescaleDev* rs, bool rs_const, uint32_t* err,
                                                       hipStream_t s) {
             ConvI8Desc d = fd;
+            if (!transposed && kern::matmul_i8_direct_applies(d.ic, d.oc, d.x, b->data->device_in())) {
+                // One kernel, B read in its own layout; the table (no weight
+                // sums: the kernel adds the a-zero-point term itself) does not
+                // depend on B's values.
+                ConvI8Desc td = d;
+                td.w = nullptr;
+                td.batch = 1;
+                auto tab = conv_i8_table_for(td, *b->data, nullptr, rs, !rs || rs_const, s);
+                if (kern::matmul_i8_direct(d.x, static_cast<const int8_t*>(b->data->device_in()), d.batch, d.ih,
+                                           d.ic, d.oc, d.zp_x, d.zp_w, tab->device_in(), rs, tab->scale_range_safe,
+                                           out, err, s))
+                    return;
+            }
             StoragePtr bt;
             if (transposed) {
                 d.w = static_cast<const int8_t*>(b->data->device_in());
