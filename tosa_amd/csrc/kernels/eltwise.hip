@@ -438,6 +438,7 @@ __global__ void __launch_bounds__(256) residual_fast_kernel(RescaleDev ra, Resca
     const uint32_t* a4 = reinterpret_cast<const uint32_t*>(a);
     const uint32_t* b4 = reinterpret_cast<const uint32_t*>(b);
     uint32_t* o4 = reinterpret_cast<uint32_t*>(out);
+#pragma unroll 2
     for (int64_t p = int64_t(blockIdx.x) * ppb + t / tpp; p < pixels; p += int64_t(gridDim.x) * ppb) {
         const int64_t q = p * tpp + cq;
         const uint32_t wa = a4[q], wb = b4[q];
@@ -755,8 +756,11 @@ void residual_add_i8(const RescaleDev& ra, const RescaleDev& rb, const RescaleDe
         const int tpp = int(channels / 4);
         const int ppb = 256 / tpp;
         const int64_t pixels = count / channels;
-        const int64_t blocks = (pixels + ppb - 1) / ppb;
-        hipLaunchKernelGGL(residual_fast_kernel, dim3(unsigned(blocks < 8192 ? blocks : 8192)), dim3(256), 0,
+        // Two workgroups per CU walk the pixels: each thread's setup (the
+        // three RESCALEs' parameters of its four channels) then serves many
+        // pixels instead of one or two.
+        const int64_t blocks = std::min<int64_t>((pixels + ppb - 1) / ppb, 2 * int64_t(cu_count()));
+        hipLaunchKernelGGL(residual_fast_kernel, dim3(unsigned(blocks)), dim3(256), 0,
                            stream, ra, rb, ro, a, b, pixels, int32_t(channels), ppb, static_cast<int8_t*>(out), err);
         return;
     }
