@@ -17,18 +17,21 @@
 // 128-byte row segments, and a conv bias is one value per lane.
 //
 // Workgroup tile 256 x 256, 8 waves of 128 (M) x 64 (N) (4 x 2 MFMA tiles,
-// 6 fragment reads per 8 MFMAs), K staged 64 elements at a time through two
-// LDS buffers. LDS image of one operand stage: the 16-byte chunk holding
+// 6 fragment reads per 8 MFMAs), K staged 32 elements at a time through a
+// ring of four LDS buffers with the direct global->LDS loads of three stages
+// in flight. LDS image of an A (or [N][K] B) stage: the 16-byte chunk holding
 // elements 16 j + 8 c .. + 7 of row r (block b = r / 32 of the tile) sits at
 // slot ((8 j + b) 2 + c) 32 + ((r % 32) ^ b), so the fragment read of a row
 // block (lane l: k-half l / 32) is one contiguous 1 KB, and lane l holds row
-// 32 b + ((l % 32) ^ b); the epilogue undoes that permutation. The XOR keeps
-// the 8-byte writes of the transposed B (eight row blocks at once) at two
-// lanes per bank.
-// A rows (and Bt rows when B is given transposed) arrive by direct
-// global->LDS loads; a [K][N] B is loaded as 4 x 8 element blocks,
-// transposed in registers with byte permutes, and written as 8-byte pieces
-// of the rows of Bt.
+// 32 b + ((l % 32) ^ b); the epilogue undoes that permutation.
+// A [K][N] B stage is copied as it lies: row k of the stage (256 columns, 32
+// 16-byte pieces) with piece p stored at p ^ (4 k % 32), and its fragments
+// are read with the LDS transpose read ds_read_b64_tr_b16: in each group of
+// 16 lanes, lane i receives element i % 4 of the 8-byte pieces addressed by
+// lanes i / 4 + 4 j (j = 0..3); lane s addresses row k0 + s / 4, columns
+// nb + 4 (s % 4), so lane i gets column nb + i of rows k0 .. k0 + 3 (the XOR
+// places the four rows and two column halves a 16-lane group reads in
+// distinct bank groups).
 #include "kcommon.h"
 
 namespace tosa {
@@ -45,9 +48,11 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lvoid;
 
 constexpr int GT = 256;        // tile rows (M) and columns (N)
-constexpr int GK = 64;         // K elements per stage
+constexpr int GK = 32;         // K elements per stage
 constexpr int GNT = 512;       // threads
-constexpr int GSTAGE = GT * GK * 2;  // bytes of one operand stage (32 KB)
+constexpr int GSTAGE = GT * GK * 2;  // bytes of one operand stage (16 KB)
+constexpr int GNS = 4;         // stages in the LDS ring
+static_assert(GNS - 2 <= 6, "vmcnt cases");
 
 struct GemmF16Args {
     const uint16_t* a;   // [batch][M][K]
@@ -63,13 +68,22 @@ struct GemmF16Args {
 
 // A direct 16-byte global->LDS load (global_load_lds_dwordx4: lane l writes
 // LDS byte address `l` + 16 l, `l` wave-uniform), issued through inline
-// assembly so that the compiler's LDS wait counting leaves the fragment
-// reads alone; the kernel waits for these loads itself (vmcnt(0) and a
-// barrier) before reading what they fill.
+// assembly so that the compiler's wait counting, which would drain every
+// such load before any LDS read, leaves the fragment reads alone; the kernel
+// counts these loads itself (s_waitcnt vmcnt) before the barrier that
+// precedes a stage's reads.
 __device__ __forceinline__ void dma16(const void* g, const void* l)
 {
     const uint32_t la = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((const lvoid*)l)));
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(la) : "memory", "m0");
+}
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+// Transposing 8-byte LDS read (see the layout note above).
+__device__ __forceinline__ v2u ldtr16(const uint8_t* p)
+{
+    const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)((const lvoid*)p));
+    return __builtin_bit_cast(v2u, r);
 }
 
 template <bool BF>
@@ -88,8 +102,8 @@ template <bool BF, bool KN>
 __global__ void __launch_bounds__(GNT, 2) gemm_f16_kernel(GemmF16Args A)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t* const sA = smem;                // [2][GSTAGE]
-    uint8_t* const sB = smem + 2 * GSTAGE;   // [2][GSTAGE]
+    uint8_t* const sA = smem;                  // [GNS][GSTAGE]
+    uint8_t* const sB = smem + GNS * GSTAGE;   // [GNS][GSTAGE]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -106,44 +120,40 @@ __global__ void __launch_bounds__(GNT, 2) gemm_f16_kernel(GemmF16Args A)
     const uint16_t* const ag = A.a + bz * A.a_bs;
     const uint16_t* const bg = A.b + bz * A.b_bs;
 
-    // ---- staging ----------------------------------------------------------
+    // ---- staging: GSTAGE / 1024 = 16 loads of 1 KB per operand, two per wave
     // DMA q fills slots 64 q .. + 63: k16 step j = q / 8, row block b = q % 8,
     // rows 32 b + ((l % 32) ^ b), k-half l / 32. Rows past the matrix re-read
     // its last row (their results are not stored).
     auto dma_rows = [&](const uint16_t* g, int rows, int r0, int k0, uint8_t* dst) {
-        for (int q = wave; q < GSTAGE / 1024; q += GNT / 64) {
+#pragma unroll
+        for (int i = 0; i < GSTAGE / 1024 / (GNT / 64); i++) {
+            const int q = wave + (GNT / 64) * i;
             const int j = q >> 3, row = 32 * (q & 7) + ((lane & 31) ^ (q & 7)), c = lane >> 5;
             const int r = r0 + row < rows ? r0 + row : rows - 1;
             dma16(g + int64_t(r) * A.K + k0 + 16 * j + 8 * c, dst + q * 1024);
         }
     };
-    // [K][N] B: thread (nb, kq) loads rows k0 + 4 kq .. + 3, columns n0 + 8 nb
-    // .. + 7 (columns past N read as zero).
-    const int nb = tid & 31, kq = tid >> 5;
-    v4u breg[4];
-    auto load_kn = [&](int k0) {
-        const int n = n0 + 8 * nb;
+    // [K][N] B: DMA q fills rows 2 q, 2 q + 1 of the stage; lane l writes
+    // piece l % 32 of row 2 q + l / 32, which holds the row's piece
+    // (l % 32) ^ (4 row % 32). Pieces past N re-read column 0 (those
+    // columns are not stored).
+    auto dma_kn = [&](int k0, uint8_t* dst) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint16_t* src = bg + int64_t(k0 + 4 * kq + i) * A.N + (n < A.N ? n : 0);
-            const v4u v = *reinterpret_cast<const v4u*>(src);
-            breg[i] = n < A.N ? v : v4u{0, 0, 0, 0};
+        for (int i = 0; i < GSTAGE / 1024 / (GNT / 64); i++) {
+            const int q = wave + (GNT / 64) * i;
+            const int row = 2 * q + (lane >> 5);
+            const int piece = (lane & 31) ^ ((4 * row) & 31);
+            const int n = n0 + 8 * piece;
+            dma16(bg + int64_t(k0 + row) * A.N + (n < A.N ? n : 0), dst + q * 1024);
         }
     };
-    auto store_kn = [&](uint8_t* dst) {
-        // k = 4 kq + i lies in chunk (j, c) = (kq / 4, (kq % 4) / 2) at byte
-        // 8 (kq % 2) + 2 i; column 8 nb + e is Bt row 8 nb + e.
-        const int j = kq >> 2, c = (kq & 3) >> 1, off = 8 * (kq & 1);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            const int d = e >> 1;
-            const uint32_t lo = __builtin_amdgcn_perm(breg[1][d], breg[0][d], sel);
-            const uint32_t hi = __builtin_amdgcn_perm(breg[3][d], breg[2][d], sel);
-            const int row = 8 * nb + e;
-            const int slot = ((8 * j + (row >> 5)) * 2 + c) * 32 + ((row & 31) ^ (row >> 5));
-            *reinterpret_cast<v2u*>(dst + slot * 16 + off) = v2u{lo, hi};
-        }
+    auto issue = [&](int st) {
+        const int slot = st % GNS;
+        dma_rows(ag, A.M, m0, st * GK, sA + slot * GSTAGE);
+        if constexpr (KN)
+            dma_kn(st * GK, sB + slot * GSTAGE);
+        else
+            dma_rows(bg, A.N, n0, st * GK, sB + slot * GSTAGE);
     };
 
     // ---- waves: 2 (M) x 4 (N), each 128 x 64 ------------------------------
@@ -155,61 +165,81 @@ __global__ void __launch_bounds__(GNT, 2) gemm_f16_kernel(GemmF16Args A)
         for (int b = 0; b < 2; b++)
             acc[a][b] = v16f{};
 
-    const int nst = A.K / GK;
-    dma_rows(ag, A.M, m0, 0, sA);
-    if constexpr (KN) {
-        load_kn(0);
-        store_kn(sB);
-    } else {
-        dma_rows(bg, A.N, n0, 0, sB);
-    }
-    for (int st = 0; st < nst; st++) {
-        const int buf = st & 1;
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (st + 1 < nst) {
-            dma_rows(ag, A.M, m0, (st + 1) * GK, sA + (buf ^ 1) * GSTAGE);
-            if constexpr (KN)
-                load_kn((st + 1) * GK);
-            else
-                dma_rows(bg, A.N, n0, (st + 1) * GK, sB + (buf ^ 1) * GSTAGE);
+    // Fragment of rows r0 .. r0 + 31 (r0 % 32 == 0) for k16 step j: one
+    // contiguous 1 KB.
+    auto frag = [&](const uint8_t* base, int j, int r0) {
+        return *reinterpret_cast<const v4u*>(base + (8 * j + (r0 >> 5)) * 1024 + lane * 16);
+    };
+    // [K][N] B fragment of columns c0 .. c0 + 31 for k16 step j: lane l gets
+    // column c0 + l % 32, elements 16 j + 8 (l / 32) .. + 7 (two transposing
+    // reads of four rows each).
+    const int trs = lane & 15, trg = lane >> 4;
+    auto frag_kn = [&](const uint8_t* base, int j, int c0) {
+        v2u h[2];
+#pragma unroll
+        for (int sub = 0; sub < 2; sub++) {
+            const int row = 16 * j + 8 * (trg >> 1) + 4 * sub + (trs >> 2);
+            const int col = c0 + 16 * (trg & 1) + 4 * (trs & 3);  // element column in the tile
+            const int piece = (col >> 3) ^ ((4 * row) & 31);
+            h[sub] = ldtr16(base + row * (GT * 2) + piece * 16 + (col & 7) * 2);
         }
-        const uint8_t* const a_s = sA + buf * GSTAGE;
-        const uint8_t* const b_s = sB + buf * GSTAGE;
-        // Fragment of rows r0 .. r0 + 31 (r0 % 32 == 0) for k16 step j: one
-        // contiguous 1 KB.
-        auto frag = [&](const uint8_t* base, int j, int r0) {
-            return *reinterpret_cast<const v4u*>(base + (8 * j + (r0 >> 5)) * 1024 + lane * 16);
-        };
-        v4u fa[2][4], fb[2][2];
+        return v4u{h[0].x, h[0].y, h[1].x, h[1].y};
+    };
+
+    const int nst = A.K / GK;
+    // GNS - 1 stages in flight; stage st's loads are the oldest outstanding
+    // ones when the wave waits for them.
+    constexpr int LPS = 2 * GSTAGE / 1024 / (GNT / 64);  // loads per stage and wave
 #pragma unroll
-        for (int a = 0; a < 4; a++)
-            fa[0][a] = frag(a_s, 0, wm + 32 * a);
-#pragma unroll
-        for (int b = 0; b < 2; b++)
-            fb[0][b] = frag(b_s, 0, wn + 32 * b);
+    for (int st = 0; st < GNS - 1; st++)
+        if (st < nst)
+            issue(st);
+    for (int st = 0; st < nst; st++) {
+        // vmcnt(N): at most N of this wave's loads outstanding, those of the
+        // later stages already issued (gfx9 s_waitcnt: vmcnt in bits 3-0 and
+        // 15-14, expcnt 6-4 and lgkmcnt 11-8 left at their maxima).
+        const int later = nst - 1 - st < GNS - 2 ? nst - 1 - st : GNS - 2;
+        switch (later) {
+#define TOSA_WAIT_VM(L)                                                                   \
+    case L:                                                                               \
+        __builtin_amdgcn_s_waitcnt(0x0F70 | ((L * LPS) & 15) | (((L * LPS) >> 4) << 14)); \
+        break;
+            TOSA_WAIT_VM(0)
+            TOSA_WAIT_VM(1)
+            TOSA_WAIT_VM(2)
+            TOSA_WAIT_VM(3)
+            TOSA_WAIT_VM(4)
+            TOSA_WAIT_VM(5)
+            TOSA_WAIT_VM(6)
+#undef TOSA_WAIT_VM
+        default:
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        // Every wave's loads of stage st have landed, and every wave is done
+        // with the buffer that stage st + GNS - 1 overwrites (stage st - 1's).
+        __syncthreads();
+        if (st + GNS - 1 < nst)
+            issue(st + GNS - 1);
+        const uint8_t* const a_s = sA + (st % GNS) * GSTAGE;
+        const uint8_t* const b_s = sB + (st % GNS) * GSTAGE;
 #pragma unroll
         for (int j = 0; j < GK / 16; j++) {
-            __builtin_amdgcn_sched_barrier(0);
-            if (j + 1 < GK / 16) {
+            v4u fa[4], fb[2];
 #pragma unroll
-                for (int a = 0; a < 4; a++)
-                    fa[(j + 1) & 1][a] = frag(a_s, j + 1, wm + 32 * a);
+            for (int a = 0; a < 4; a++)
+                fa[a] = frag(a_s, j, wm + 32 * a);
 #pragma unroll
-                for (int b = 0; b < 2; b++)
-                    fb[(j + 1) & 1][b] = frag(b_s, j + 1, wn + 32 * b);
+            for (int b = 0; b < 2; b++) {
+                if constexpr (KN)
+                    fb[b] = frag_kn(b_s, j, wn + 32 * b);
+                else
+                    fb[b] = frag(b_s, j, wn + 32 * b);
             }
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int b = 0; b < 2; b++)
 #pragma unroll
                 for (int a = 0; a < 4; a++)
-                    acc[a][b] = mfma32<BF>(fa[j & 1][a], fb[j & 1][b], acc[a][b]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (KN) {
-            if (st + 1 < nst)
-                store_kn(sB + (buf ^ 1) * GSTAGE);
+                    acc[a][b] = mfma32<BF>(fa[a], fb[b], acc[a][b]);
         }
     }
 
@@ -219,7 +249,7 @@ __global__ void __launch_bounds__(GNT, 2) gemm_f16_kernel(GemmF16Args A)
 #pragma unroll
     for (int b = 0; b < 2; b++) {
         const int nblk = (wn >> 5) + b;  // row block of Bt in the tile
-        const int n = n0 + 32 * nblk + ((lane & 31) ^ nblk);
+        const int n = n0 + 32 * nblk + (KN ? (lane & 31) : ((lane & 31) ^ nblk));
         if (n >= A.N)
             continue;
         const bool has_bias = A.bias != nullptr;
@@ -246,7 +276,7 @@ __global__ void __launch_bounds__(GNT, 2) gemm_f16_kernel(GemmF16Args A)
     }
 }
 
-constexpr int GLDS = 4 * GSTAGE;  // 128 KB
+constexpr int GLDS = 2 * GNS * GSTAGE;  // 128 KB
 
 template <bool BF, bool KN>
 void launch(const GemmF16Args& a, hipStream_t s)
