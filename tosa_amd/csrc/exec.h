@@ -48,6 +48,10 @@ struct FusionPlan {
     std::vector<int> residual_tail;
     // RESCALE op whose output feeds such an ADD only
     std::vector<bool> residual_input;
+    // Convolution whose fused RESCALE (no CLAMP) feeds only such a residual
+    // RESCALE: its launch may wait for the ADD and carry the residual in its
+    // epilogue
+    std::vector<bool> residual_head;
 
     static FusionPlan build(const BasicBlock& b);
 };

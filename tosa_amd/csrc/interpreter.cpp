@@ -45,6 +45,7 @@ FusionPlan FusionPlan::build(const BasicBlock& b)
     p.clamp_after.assign(n, -1);
     p.residual_tail.assign(n, -1);
     p.residual_input.assign(n, false);
+    p.residual_head.assign(n, false);
 
     std::unordered_map<std::string, std::vector<int>> consumers;  // name -> consuming ops (one entry per use)
     std::unordered_map<std::string, int> producers;
@@ -103,6 +104,16 @@ FusionPlan FusionPlan::build(const BasicBlock& b)
                 p.residual_input[ins[1]] = true;
             }
         }
+    }
+    // A convolution whose fused RESCALE result (no CLAMP after it) is read
+    // only by a residual RESCALE.
+    for (size_t i = 0; i < n; i++) {
+        const int j = p.rescale_after[i];
+        if (b.operators[i].op != OP_CONV2D || j < 0 || p.clamp_after[j] >= 0 || b.operators[j].outputs.size() != 1)
+            continue;
+        const int k = sole_first_use(b.operators[j].outputs[0], OP_RESCALE);
+        if (k >= 0 && p.residual_input[k])
+            p.residual_head[i] = true;
     }
     return p;
 }

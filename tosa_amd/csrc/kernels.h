@@ -103,6 +103,13 @@ struct ConvI8Desc {
     // The epilogue table proved that no value can fail apply_scale_32's
     // range REQUIRE (conv_i8_table_range_safe), so the kernels skip it.
     bool range_safe = false;
+    // Quantised residual folded into the epilogue (conv_i8_residual_ok):
+    // the int8 result y of the fused RESCALE goes on through
+    // RESCALE(y) + RESCALE(skip) -> ADD -> RESCALE, and only that is stored.
+    const int8_t* res_skip = nullptr;  // [pixels][oc] int8, the other ADD operand's source
+    const void* res_tab = nullptr;     // conv_i8_residual_table output
+    int32_t res_za = 0, res_zb = 0;    // input zero points of RESCALE(y) and RESCALE(skip)
+    int32_t res_clo = 0, res_chi = 0;  // final output range (the last RESCALE's, narrowed to its CLAMP)
 };
 // Geometry and alignment the kernels handle: CONV2D 1x1 stride-1 unpadded
 // with ic % 16 == 0, any other CONV2D geometry with ic % 64 == 0;
@@ -114,6 +121,19 @@ bool conv_i8_fast_supported(const ConvI8Desc& d);
 // and an output zero point the table can fold into its rounding constants
 // (|zp| 2^max_shift <= 2^60).
 bool conv_i8_fast_epilogue_ok(const RescaleDev& rs);
+// Whether a 1x1 stride-1 int8 CONV2D whose fused RESCALE `rs` gives int8
+// (no CLAMP) can carry the quantised residual RESCALE(y; ra) +
+// RESCALE(skip; rb) -> ADD -> RESCALE(ro) in its epilogue: ra and rb int8
+// -> int32 with shifts >= 9 (so their REQUIREs cannot fail), ro int32 ->
+// int8 with SINGLE/DOUBLE rounding and a foldable output zero point, a
+// multiple of 4 and at most 1024 channels, a 4-byte aligned skip tensor.
+bool conv_i8_residual_ok(const ConvI8Desc& d, const RescaleDev& rs, const RescaleDev& ra, const RescaleDev& rb,
+                         const RescaleDev& ro, const void* skip);
+// Per-channel constants of the three residual RESCALEs, built on the device
+// (CONV_I8_RES_WORDS int32 per channel).
+constexpr int CONV_I8_RES_WORDS = 20;
+void conv_i8_residual_table(const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro, int32_t channels,
+                            void* out, hipStream_t stream);
 // Per-channel epilogue table (8 int32 per output channel, then 4 int32 of
 // the input zero point's byte, then one int32 per channel) built on the
 // device from w, bias, the zero points and, when `rs` is given, the RESCALE

@@ -58,6 +58,12 @@ struct EpiArgs {
     // Some channel's shift is below 32, so apply_scale_32's value-range
     // REQUIRE can fail and is checked (with every shift >= 32 it cannot).
     int32_t range;
+    // Quantised residual in the epilogue (kernels instantiated with it): the
+    // skip tensor (same layout as the output), the input zero points of its
+    // two int8 -> int32 RESCALEs, and the final output range (the last
+    // RESCALE's type range, narrowed to a fused CLAMP).
+    const int8_t* skip;
+    int32_t za, zb, rclo, rchi;
 };
 
 
@@ -74,6 +80,7 @@ struct ConvI8Args {
     // of the table in 16-byte entries.
     int64_t bsx, bsw, bso;
     int32_t bst, batch;
+    const int32_t* rtab;  // residual constants, CONV_I8_RES_WORDS per channel (RES kernels)
 };
 
 // Median of three (v_med3_i32): clamp of v to [lo, hi] when lo <= hi.
@@ -103,13 +110,40 @@ __device__ __forceinline__ int swz(int row)
 // consecutive channels starting at tile channel `cl0` of tile pixel
 // wave_p0 + 16 tn + j16; `pixel(p)` maps a tile pixel to its output row
 // (NHWC pixel index) or -1 when the pixel does not exist.
-template <int TM, int TN, int OB, bool RS, bool ZW, bool RC, typename PixelMap>
-__device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, const int32_t* s_rowsum, int cl0,
-                                         int n0, int wave_p0, int j16, const EpiArgs& E, PixelMap pixel)
+// apply_scale_32 of a residual RESCALE with per-channel constants m, s and
+// the sign-selected rounding constant (output zero point folded in).
+__device__ __forceinline__ int32_t res_apply(int32_t x, int32_t m, int32_t s, int64_t rp, int64_t rn)
 {
+    return int32_t((int64_t(x) * m + (x >= 0 ? rp : rn)) >> s);
+}
+
+// RES: the RESCALE result y (int8) goes on through the quantised residual:
+// y' = RESCALE(RESCALE(y - za) + RESCALE(skip - zb)) with the constants of
+// s_res (CONV_I8_RES_WORDS per tile channel: m, s, rp, rn of each of the
+// three RESCALEs, then the last one's value-range bound), and y' is stored.
+template <int TM, int TN, int OB, bool RS, bool ZW, bool RC, bool RES = false, typename PixelMap>
+__device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, const int32_t* s_rowsum, int cl0,
+                                         int n0, int wave_p0, int j16, const EpiArgs& E, PixelMap pixel,
+                                         const int32_t* s_res = nullptr)
+{
+    static_assert(!RES || (RS && OB == 1), "the residual follows an int8 RESCALE");
     constexpr int WORDS = TM * OB;  // 32-bit words of output per lane and pixel
     const int c0 = n0 + cl0;
     uint32_t res[TN][WORDS];
+    // Skip bytes of this lane's channels (four per word), loaded up front.
+    uint32_t skw[RES ? TN : 1][RES ? TM : 1];
+    uint32_t res_bad = 0;
+    if constexpr (RES) {
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            const int m = pixel(wave_p0 + 16 * tn + j16);
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+                skw[tn][tm] = m >= 0 && c0 + 4 * tm < E.N
+                                  ? *reinterpret_cast<const uint32_t*>(E.skip + int64_t(m) * E.N + c0 + 4 * tm)
+                                  : 0u;
+        }
+    }
     // Nonzero when a value fails apply_scale_32's range REQUIRE (one bitwise
     // op per value on the VALU).
     uint32_t bad_bits = 0;
@@ -126,6 +160,22 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
             if constexpr (RS)
                 t1[i] = s_tab[2 * (cl0 + 4 * tm + i) + 1];
             hi[i] = ~t0[i].z;
+        }
+        // The group's residual constants (words 0-18 of each channel).
+        int32_t rq[4][RES ? 20 : 1];
+        if constexpr (RES) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const v4i* q = reinterpret_cast<const v4i*>(s_res + CONV_I8_RES_WORDS * (cl0 + 4 * tm + i));
+#pragma unroll
+                for (int k = 0; k < 5; k++) {
+                    const v4i v = q[k];
+                    rq[i][4 * k] = v.x;
+                    rq[i][4 * k + 1] = v.y;
+                    rq[i][4 * k + 2] = v.z;
+                    rq[i][4 * k + 3] = v.w;
+                }
+            }
         }
 #pragma unroll
         for (int tn = 0; tn < TN; tn++) {
@@ -159,6 +209,27 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
                     v[i] = med3(r, E.clo, E.chi);
                 } else {
                     v[i] = x;
+                }
+            }
+            if constexpr (RES) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int32_t* q = rq[i];
+                    const int64_t rpa = __builtin_bit_cast(int64_t, v2i{q[2], q[3]});
+                    const int64_t rna = __builtin_bit_cast(int64_t, v2i{q[4], q[5]});
+                    const int64_t rpb = __builtin_bit_cast(int64_t, v2i{q[8], q[9]});
+                    const int64_t rnb = __builtin_bit_cast(int64_t, v2i{q[10], q[11]});
+                    const int64_t rpo = __builtin_bit_cast(int64_t, v2i{q[14], q[15]});
+                    const int64_t rno = __builtin_bit_cast(int64_t, v2i{q[16], q[17]});
+                    const int32_t va = res_apply(v[i] - E.za, q[0], q[1], rpa, rna);
+                    const int32_t sb = int32_t(int8_t(skw[tn][tm] >> (8 * i)));
+                    const int32_t vb = res_apply(sb - E.zb, q[6], q[7], rpb, rnb);
+                    const int32_t sum = int32_t(uint32_t(va) + uint32_t(vb));
+                    // apply_scale_32's value-range REQUIRE of the last RESCALE
+                    // (q[18] = -2^min(s - 1, 31)).
+                    res_bad = __builtin_amdgcn_bitop3_b32(res_bad, uint32_t(med3(sum, q[18], ~q[18])),
+                                                          uint32_t(sum), 0xf6);
+                    v[i] = med3(res_apply(sum, q[12], q[13], rpo, rno), E.rclo, E.rchi);
                 }
             }
             if constexpr (OB == 1) {
@@ -217,7 +288,7 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
             }
         }
     }
-    if (bad_bits)
+    if (bad_bits | res_bad)
         atomicOr(E.err, DERR_SCALE_RANGE);
 }
 
@@ -225,7 +296,7 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
 // unpadded convolution (a plain GEMM over the NHWC rows; K may be any
 // multiple of 16). OB: output bytes (1, 2, 4). RS: RESCALE epilogue (else
 // int32 + bias). ZW: weight zero point is nonzero.
-template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW>
+template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW, bool RES = false>
 __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args Ain)
 {
     ConvI8Args A = Ain;
@@ -344,11 +415,19 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args Ain)
         }
     };
 
-    // The tile's epilogue table, staged in LDS behind the stage buffers.
+    // The tile's epilogue table, staged in LDS behind the stage buffers
+    // (with RES, the residual constants behind it).
     v4i* const s_tab = reinterpret_cast<v4i*>(smem + 2 * (BC + BP) * KC);
     for (int i = tid; i < 2 * BC; i += 256) {
         const int c = n0 + (i >> 1);
         s_tab[i] = A.tab[2 * (c < A.N ? c : A.N - 1) + (i & 1)];
+    }
+    int32_t* const s_res = reinterpret_cast<int32_t*>(s_tab + 2 * BC);
+    if constexpr (RES) {
+        for (int i = tid; i < CONV_I8_RES_WORDS * BC; i += 256) {
+            const int c = n0 + i / CONV_I8_RES_WORDS;
+            s_res[i] = A.rtab[(c < A.N ? c : A.N - 1) * CONV_I8_RES_WORDS + i % CONV_I8_RES_WORDS];
+        }
     }
 
     v4i acc[TM][TN];
@@ -435,11 +514,11 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args Ain)
     if (wave_live) {
         auto pixel = [&](int p) { return m0 + p < A.M ? m0 + p : -1; };
         if (!RS || A.E.range)
-            epilogue<TM, TN, OB, RS, ZW, true>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
-                                               pixel);
+            epilogue<TM, TN, OB, RS, ZW, true, RES>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16,
+                                                    A.E, pixel, s_res);
         else
-            epilogue<TM, TN, OB, RS, ZW, false>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16, A.E,
-                                                pixel);
+            epilogue<TM, TN, OB, RS, ZW, false, RES>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, n0, wave_p0, j16,
+                                                     A.E, pixel, s_res);
     }
 }
 
@@ -2621,11 +2700,12 @@ bool pws_applies(const ConvI8Desc& d, bool pw, int ob, const RescaleDev* rs)
            m * d.ic < (int64_t(1) << 31);
 }
 
-template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW>
+template <int BC, int BP, int WC, int WP, int KC, bool PW, int OB, bool RS, bool ZW, bool RES = false>
 void launch(const ConvI8Args& a, hipStream_t s)
 {
-    auto kfn = conv_i8_kernel<BC, BP, WC, WP, KC, PW, OB, RS, ZW>;
-    constexpr size_t lds = size_t(2) * (BC + BP) * KC + size_t(32) * BC;
+    auto kfn = conv_i8_kernel<BC, BP, WC, WP, KC, PW, OB, RS, ZW, RES>;
+    constexpr size_t lds =
+        size_t(2) * (BC + BP) * KC + size_t(32) * BC + (RES ? size_t(4) * CONV_I8_RES_WORDS * BC : 0);
     static_assert(lds >= 4 * BP, "rowsum scratch");
     static bool attr = [&]() {
         hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2639,8 +2719,18 @@ void launch(const ConvI8Args& a, hipStream_t s)
 }
 
 template <int BC, int BP, int WC, int WP, int KC, bool PW>
-void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
+void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s, bool res = false)
 {
+    if constexpr (PW) {
+        if (res) {
+            // The quantised residual follows an int8 RESCALE (host-checked).
+            if (zw)
+                launch<BC, BP, WC, WP, KC, PW, 1, true, true, true>(a, s);
+            else
+                launch<BC, BP, WC, WP, KC, PW, 1, true, false, true>(a, s);
+            return;
+        }
+    }
     if (!rs) {
         if (zw)
             launch<BC, BP, WC, WP, KC, PW, 4, false, true>(a, s);
@@ -2668,7 +2758,7 @@ void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
 // per-output work dominates layers with few reduction steps. Pointwise
 // layers weigh the input's re-reads per channel block instead.
 template <int KC, bool PW>
-void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
+void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s, bool res = false)
 {
     const int64_t n = a.N;
     const int64_t w128 = (n + 63) / 64 * 64, w64 = (n + 63) / 64 * 64, w32 = (n + 31) / 32 * 32,
@@ -2686,13 +2776,13 @@ void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
             if (cost[i] < cost[best])
                 best = i;
         if (best == 0)
-            launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s, res);
         else if (best == 1)
-            launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else if (best == 2)
-            launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
-            launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         return;
     }
     // Over few pixels a pointwise layer's 256-pixel tiles leave most CUs
@@ -2701,22 +2791,22 @@ void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s)
     const int64_t wgs_needed = 2 * int64_t(cu_count());
     auto few = [&](int64_t bc) { return PW && (int64_t(a.M) + 255) / 256 * ((n + bc - 1) / bc) < wgs_needed; };
     if (w128 <= w32 && w128 <= w16 && n > 64)
-        launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s);
+        launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s, res);
     else if (w64 <= w32 && w64 <= w16 && n > 32) {
         if (few(64))
-            launch_epi<64, 64, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<64, 64, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
-            launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
     } else if (w32 <= w16 && n > 16) {
         if (few(32))
-            launch_epi<32, 64, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<32, 64, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
-            launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
     } else {
         if (few(16))
-            launch_epi<16, 64, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<16, 64, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
-            launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s);
+            launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
     }
 }
 
@@ -3084,6 +3174,77 @@ void launch_dw_epi(const DwArgs& a, int ob, bool rs, bool zw, hipStream_t s)
 }
 
 }  // namespace
+
+namespace {
+// Residual constants of channel c: for each of RESCALE(y), RESCALE(skip)
+// and the final RESCALE, {m, s, rp (2 words), rn (2 words)} with the
+// sign-selected rounding constants of apply_scale_32 (the last one carrying
+// its output zero point), then -2^min(s - 1, 31) of the final RESCALE.
+__global__ void conv_i8_residual_table_kernel(RescaleDev ra, RescaleDev rb, RescaleDev ro, int32_t channels,
+                                              int32_t* out)
+{
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= channels)
+        return;
+    int32_t* q = out + int64_t(c) * CONV_I8_RES_WORDS;
+    auto put = [&](const RescaleDev& r, int64_t zp, int32_t* w) {
+        const int ch = r.per_channel ? c : 0;
+        const int32_t m = r.mult[ch], s = r.shift[ch];
+        const int64_t half = int64_t(1) << (s - 1);
+        const int64_t d = (r.rounding == 3 && s > 31) ? (int64_t(1) << 30) : 0;
+        const int64_t z = zp * (int64_t(1) << s);
+        const int64_t rp = half + d + z, rn = half - d + z;
+        w[0] = m;
+        w[1] = s;
+        w[2] = int32_t(uint64_t(rp));
+        w[3] = int32_t(uint64_t(rp) >> 32);
+        w[4] = int32_t(uint64_t(rn));
+        w[5] = int32_t(uint64_t(rn) >> 32);
+        return s;
+    };
+    put(ra, 0, q);
+    put(rb, 0, q + 6);
+    const int32_t so = put(ro, ro.out_zp, q + 12);
+    q[18] = so - 1 < 31 ? -(int32_t(1) << (so - 1)) : INT32_MIN;
+    q[19] = 0;
+}
+}  // namespace
+
+void conv_i8_residual_table(const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro, int32_t channels,
+                            void* out, hipStream_t stream)
+{
+    if (channels <= 0)
+        return;
+    hipLaunchKernelGGL(conv_i8_residual_table_kernel, dim3(unsigned((channels + 255) / 256)), dim3(256), 0, stream,
+                       ra, rb, ro, channels, static_cast<int32_t*>(out));
+}
+
+bool conv_i8_residual_ok(const ConvI8Desc& d, const RescaleDev& rs, const RescaleDev& ra, const RescaleDev& rb,
+                         const RescaleDev& ro, const void* skip)
+{
+    const bool pw = !d.depthwise && d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 &&
+                    d.ih == d.oh && d.iw == d.ow;
+    const int64_t ch = d.oc;
+    // The input RESCALEs: int8 -> int32, SINGLE/DOUBLE rounding, shifts >= 9
+    // (|x - zp| <= 255 < 2^(s-1): the range REQUIRE holds, and the scaled
+    // value fits int32), no output zero point or CLAMP.
+    auto in_ok = [ch](const RescaleDev& r) {
+        return r.scale32 && (r.rounding == 1 || r.rounding == 3) && r.in_bits == 8 && !r.in_unsigned &&
+               r.out_bytes == 4 && r.out_zp == 0 && !r.has_clamp && r.min_shift >= 9 &&
+               (!r.per_channel || r.channels == ch);
+    };
+    // The final RESCALE: int32 -> int8 with an output zero point the
+    // rounding constants can carry (|zp| 2^s <= 2^60).
+    const int64_t zp = ro.out_zp < 0 ? -ro.out_zp : ro.out_zp;
+    const bool fold = zp == 0 || (ro.max_shift <= 60 && zp <= (int64_t(1) << (60 - ro.max_shift)));
+    const bool o_ok = ro.scale32 && (ro.rounding == 1 || ro.rounding == 3) && ro.in_bits == 32 && !ro.in_unsigned &&
+                      ro.in_zp == 0 && ro.out_bytes == 1 && fold && (!ro.per_channel || ro.channels == ch);
+    // The convolution's own RESCALE gives int8 without a CLAMP.
+    const bool y_ok = conv_i8_fast_epilogue_ok(rs) && rs.out_bytes == 1 && !rs.has_clamp && rs.lo == -128 &&
+                      rs.hi == 127;
+    return pw && d.batch == 1 && conv_i8_fast_supported(d) && y_ok && in_ok(ra) && in_ok(rb) && o_ok &&
+           ch % 4 == 0 && ch <= 1024 && reinterpret_cast<uintptr_t>(skip) % 4 == 0;
+}
 
 bool matmul_i8_direct_applies(int32_t C, int32_t W, const void* a, const void* b)
 {
@@ -3475,7 +3636,15 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
     }
     const bool pw = d.kh == 1 && d.kw == 1 && d.sy == 1 && d.sx == 1 && d.pt == 0 && d.pl == 0 && d.ih == d.oh &&
                     d.iw == d.ow;
-    if (pws_applies(d, pw, ob, rs)) {
+    const bool res = d.res_skip != nullptr;
+    if (res) {
+        e.skip = d.res_skip;
+        e.za = d.res_za;
+        e.zb = d.res_zb;
+        e.rclo = d.res_clo;
+        e.rchi = d.res_chi;
+    }
+    if (!res && pws_applies(d, pw, ob, rs)) {
         PwsArgs a{};
         a.x = d.x;
         a.w = d.w;
@@ -3592,10 +3761,11 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
         // 256; 144 -> 24 at 56 x 56: 18.3 -> 13.6 us). For longer K the extra
         // steps cost more than the padding (K = 960 over 7 x 7 images: 3-4 us
         // slower with 64).
+        a.rtab = static_cast<const int32_t*>(d.res_tab);
         if (a.K >= 192 || a.K == 128)
-            launch_tile<128, true>(a, ob, rs != nullptr, zw, stream);
+            launch_tile<128, true>(a, ob, rs != nullptr, zw, stream, res);
         else
-            launch_tile<64, true>(a, ob, rs != nullptr, zw, stream);
+            launch_tile<64, true>(a, ob, rs != nullptr, zw, stream, res);
     } else if (d.ic % 128 == 0) {
         launch_tile<128, false>(a, ob, rs != nullptr, zw, stream);
     } else {

@@ -470,6 +470,18 @@ ClampPrep prepare_clamp_int(const ExecState& st, const Operator& op, const Tenso
     return c;
 }
 
+// A convolution whose int8 RESCALE result feeds a quantised residual, with
+// its launch held back (the result is a virtual tensor carrying this): the
+// ADD of the residual launches it with the residual in its epilogue when
+// conv_i8_residual_ok admits the three RESCALEs; `launch` returns false
+// otherwise (nothing launched).
+struct ConvResRecipe {
+    std::function<bool(void* out, const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro, bool cacheable,
+                       const int8_t* skip, uint32_t* err, hipStream_t s)>
+        launch;
+};
+constexpr int AUX_CONV_RES = 101;
+
 // The RESCALE (and CLAMP) that follow an int32 producer, prepared for a
 // fused epilogue; nullopt when the chain cannot be fused.
 struct FusedTail {
@@ -990,6 +1002,57 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             }
         };
         if (auto tail = plan_tail(st, index, g.out_shape)) {
+            if (fast && count > 0 && !tail->cop && st.plan->residual_head[index] && tail->rp.out_t == DT_INT8) {
+                // The result y only feeds a residual: hold the launch back
+                // for the ADD, which may fold the residual into it.
+                const bool rs_const = st.is_const(tail->rop->inputs[1]) && st.is_const(tail->rop->inputs[2]);
+                const RescaleDev rsj = tail->rp.rs;
+                auto keep = tail->rp.params;
+                auto head = virtual_output(out_name, g.out_shape, DT_INT32, [launch, keep](Storage& o) {
+                    Stream& s = thread_stream();
+                    launch(o.device_out(), nullptr, false, s.err, s.s);
+                });
+                st.set(head);
+                auto y = virtual_output(tail->rop->outputs[0], g.out_shape, DT_INT8,
+                                        [launch, keep, rsj, rs_const](Storage& o) {
+                                            Stream& s = thread_stream();
+                                            launch(o.device_out(), &rsj, rs_const, s.err, s.s);
+                                        });
+                auto recipe = std::make_shared<ConvResRecipe>();
+                recipe->launch = [fd, weight, bias, w_const, wb_const, rsj, rs_const, keep, x](
+                                     void* out, const RescaleDev& ra, const RescaleDev& rb, const RescaleDev& ro,
+                                     bool cacheable, const int8_t* skip, uint32_t* err, hipStream_t s) {
+                    if (!conv_i8_residual_ok(fd, rsj, ra, rb, ro, skip))
+                        return false;
+                    (void)x;
+                    auto tab = conv_i8_table_for(fd, *weight->data, bias->data.get(), &rsj, wb_const && rs_const, s);
+                    char key[192];
+                    std::snprintf(key, sizeof key, "conv_i8_res:%p:%p:%p:%p:%p:%p:%d:%d:%d:%d:%d:%d:%lld",
+                                  static_cast<const void*>(ra.mult), static_cast<const void*>(ra.shift),
+                                  static_cast<const void*>(rb.mult), static_cast<const void*>(rb.shift),
+                                  static_cast<const void*>(ro.mult), static_cast<const void*>(ro.shift),
+                                  ra.per_channel, rb.per_channel, ro.per_channel, ra.rounding, rb.rounding,
+                                  ro.rounding, static_cast<long long>(ro.out_zp));
+                    auto rtab = derived_i8(*weight->data, key, int64_t(fd.oc) * CONV_I8_RES_WORDS * 4,
+                                           w_const && cacheable, s, [&](void* dst) {
+                                               conv_i8_residual_table(ra, rb, ro, fd.oc, dst, s);
+                                           });
+                    ConvI8Desc f = fd;
+                    f.range_safe = tab->scale_range_safe;
+                    f.res_skip = skip;
+                    f.res_tab = rtab->device_in();
+                    f.res_za = int32_t(ra.in_zp);
+                    f.res_zb = int32_t(rb.in_zp);
+                    f.res_clo = int32_t(ro.has_clamp ? std::max<int64_t>(ro.clamp_lo, ro.lo) : ro.lo);
+                    f.res_chi = int32_t(ro.has_clamp ? std::min<int64_t>(ro.clamp_hi, ro.hi) : ro.hi);
+                    conv_i8_fast(f, tab->device_in(), &rsj, out, err, s);
+                    return true;
+                };
+                y->data->aux = std::shared_ptr<Storage>(recipe, reinterpret_cast<Storage*>(recipe.get()));
+                y->data->aux_kind = AUX_CONV_RES;
+                st.pending[tail->rop->outputs[0]] = y;
+                return;
+            }
             const DType final_t = tail->rp.out_t;
             auto fin = new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], g.out_shape, final_t);
             const bool rs_const =
@@ -1623,6 +1686,7 @@ void eval_avg_pool2d(ExecState& st, const Operator& op)
 struct RescaleRecipe {
     TensorPtr src;
     RescalePrep rp;
+    bool consts = false;  // multiplier and shift are graph constants
 };
 
 // ---------------------------------------------------------------------------
@@ -1938,6 +2002,7 @@ void eval_rescale(ExecState& st, const Operator& op, size_t index)
         auto recipe = std::make_shared<RescaleRecipe>();
         recipe->src = input;
         recipe->rp = p;
+        recipe->consts = st.is_const(op.inputs[1]) && st.is_const(op.inputs[2]);
         // The recipe rides on the virtual storage as an opaque aux entry.
         out->data->aux = std::shared_ptr<Storage>(recipe, reinterpret_cast<Storage*>(recipe.get()));
         out->data->aux_kind = 100;
@@ -2073,10 +2138,30 @@ void eval_add(ExecState& st, const Operator& op, size_t index)
             if (tail && tail->out_t == DT_INT8) {
                 auto fin = new_output(rop.outputs[0], out, DT_INT8);
                 void* fo = fin->data->device_out();
-                kern::residual_add_i8(ra->rp.rs, rb->rp.rs, tail->rs,
-                                      static_cast<const int8_t*>(ra->src->data->device_in()),
-                                      static_cast<const int8_t*>(rb->src->data->device_in()), count, out.back(), fo,
-                                      st.err(), st.s());
+                // A held-back convolution as either operand's source takes
+                // the residual into its epilogue; otherwise the residual
+                // kernel reads both int8 sources.
+                auto conv_of = [](const TensorPtr& x) -> ConvResRecipe* {
+                    if (x->data->is_virtual() && x->data->aux_kind == AUX_CONV_RES)
+                        return reinterpret_cast<ConvResRecipe*>(x->data->aux.get());
+                    return nullptr;
+                };
+                const bool cacheable =
+                    ra->consts && rb->consts && st.is_const(rop.inputs[1]) && st.is_const(rop.inputs[2]);
+                bool done = false;
+                for (int side = 0; side < 2 && !done; side++) {
+                    RescaleRecipe* ry = side == 0 ? ra : rb;
+                    RescaleRecipe* rx = side == 0 ? rb : ra;
+                    ConvResRecipe* cr = conv_of(ry->src);
+                    if (cr && !conv_of(rx->src))
+                        done = cr->launch(fo, ry->rp.rs, rx->rp.rs, tail->rs, cacheable,
+                                          static_cast<const int8_t*>(rx->src->data->device_in()), st.err(), st.s());
+                }
+                if (!done)
+                    kern::residual_add_i8(ra->rp.rs, rb->rp.rs, tail->rs,
+                                          static_cast<const int8_t*>(ra->src->data->device_in()),
+                                          static_cast<const int8_t*>(rb->src->data->device_in()), count, out.back(),
+                                          fo, st.err(), st.s());
                 BroadcastDesc bd{};
                 bd.rank = int32_t(rank);
                 int64_t s = 1;
