@@ -168,8 +168,12 @@ tosa_status tosa_run_graph_with_hooks(const uint8_t* data, size_t len, tosa_tens
  * value-dependent REQUIRE failures (RESCALE range/overflow) of such runs are
  * reported by the next tosa_synchronize. Validation errors are unaffected.
  * "conv_rows" (default 1, process-wide): int8 3x3 stride-1 CONV2D with 128
- * input channels and 17-30 pixel output rows runs on the row-tile kernel;
- * 0 selects the halo kernel. Both are bit-exact. */
+ * input channels and 17-30 pixel output rows runs on the row-tile kernel
+ * (128-channel workgroups where the channels allow); 2 keeps the row-tile
+ * kernel at 64-channel workgroups; 0 selects the halo kernel. All are
+ * bit-exact.
+ * "matmul_rows" (default 128, process-wide): rows of A per workgroup of the
+ * int8 MATMUL kernel, 128 or 64; both are bit-exact. */
 tosa_status tosa_set_option(const char* key, int value);
 int tosa_get_option(const char* key);
 /* Run this thread's work on `hip_stream` (a hipStream_t); NULL restores the

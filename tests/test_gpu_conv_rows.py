@@ -14,7 +14,7 @@ RESCALE to int8 and int16 with per-channel and per-tensor SINGLE/DOUBLE
 rounding and output zero points, a fused CLAMP, and shifts below 32 with
 biases the table cannot prove safe (apply_scale_32's value-range REQUIRE
 checked per value: passing, and failing). The halo kernel (option
-conv_rows 0) must give the same bits.
+conv_rows 0) and 64-channel workgroups (conv_rows 2) must give the same bits.
 """
 
 import numpy as np
@@ -72,17 +72,21 @@ def test_rows_conv(case, mode):
     check(graph, out, ins)
 
 
-@pytest.mark.parametrize("case", [0, 2])
-def test_rows_matches_halo_kernel(case):
+@pytest.mark.parametrize("case", [0, 2, 4])
+@pytest.mark.parametrize("other", [0, 2])
+def test_rows_matches_other_kernels(case, other):
+    # conv_rows 0: the halo kernel; 2: the row-tile kernel at 64-channel
+    # workgroups for channel counts that allow 128.
     (graph, out), x = _case(case, "rescale_i8")
     ins = {"x": (x, "INT8")}
     rows = run(graph, ins)[out].numpy()
-    T.set_option("conv_rows", 0)
+    T.set_option("conv_rows", other)
     try:
-        halo = run(graph, ins)[out].numpy()
+        assert T.get_option("conv_rows") == other
+        alt = run(graph, ins)[out].numpy()
     finally:
         T.set_option("conv_rows", 1)
-    assert np.array_equal(rows, halo)
+    assert np.array_equal(rows, alt)
 
 
 def test_rows_range_require_failure():

@@ -1,19 +1,19 @@
 """GPU parity of the one-kernel int8 MATMUL (matmul_i8_kernel in
-tosa_amd/csrc/kernels/conv_i8.hip: B read in its [C][W] layout and transposed
-in registers, the zero-point terms from the staged bytes) against the oracle,
-bit for bit.
+tosa_amd/csrc/kernels/conv_i8.hip: A and B copied to LDS as they lie, B's
+column fragments read with LDS transpose reads, the zero-point terms from the
+fragments) against the oracle, bit for bit.
 
 The kernel takes C a multiple of 128 and W a multiple of 16. The cases pick
-what its indexing depends on: H below, at and past the 64-row tile (rows of
-the last tile re-read row H - 1 and are not stored); W below, at and past the
-128-column tile (the last column piece re-reads the final 16 columns); one,
-two, three and eight 128-byte stages (the two register sets and LDS buffers
-alternate, odd counts end on the first); every combination of zero and
-nonzero zero points (row sums of A, column sums of B, both, neither); int32
-output and the fused RESCALE to int8 and int16 with per-tensor and
-per-channel parameters, an output zero point and a CLAMP; shifts below 32
-(apply_scale_32's value-range REQUIRE checked per value, passing and
-failing). Results of the fused and unfused graphs must agree as well.
+what its indexing depends on: workgroups of 64 and of 128 rows (option
+matmul_rows); H below, at and past the row tile (rows of the last tile
+re-read row H - 1 and are not stored); W below, at and past the 128-column
+tile (the last column piece re-reads the final 16 columns); one to five and
+eight 128-byte stages (rings of three and of four LDS buffers); every combination of zero and nonzero zero points (row
+sums of A, column sums of B, both, neither); int32 output and the fused
+RESCALE to int8 and int16 with per-tensor and per-channel parameters, an
+output zero point and a CLAMP; shifts below 32 (apply_scale_32's value-range
+REQUIRE checked per value, passing and failing). Results of the fused and
+unfused graphs must agree as well.
 """
 
 import numpy as np
@@ -33,7 +33,17 @@ DIMS = [
     (3, 100, 256, 208),
     (1, 7, 384, 1040),
     (2, 130, 1024, 144),
+    (1, 200, 512, 96),
+    (2, 33, 640, 48),
 ]
+
+
+@pytest.fixture(params=[64, 128], autouse=True)
+def tile_rows(request):
+    T.set_option("matmul_rows", request.param)
+    assert T.get_option("matmul_rows") == request.param
+    yield request.param
+    T.set_option("matmul_rows", 128)
 ZPS = [(0, 0), (-7, 2), (127, -128), (0, 5), (-3, 0)]
 
 

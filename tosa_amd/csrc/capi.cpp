@@ -560,7 +560,9 @@ tosa_status tosa_set_option(const char* key, int value)
     else if (std::strcmp(key, "deferred") == 0)
         o.deferred = value != 0;
     else if (std::strcmp(key, "conv_rows") == 0)
-        kern::set_conv_rows_enabled(value != 0);
+        kern::set_conv_rows_mode(value);
+    else if (std::strcmp(key, "matmul_rows") == 0)
+        kern::set_mm_tile_rows(value);
     else
         return fail(TOSA_ERR_INVALID_ARGUMENT, std::string("unknown option ") + key);
     return TOSA_OK;
@@ -578,7 +580,9 @@ int tosa_get_option(const char* key)
     if (std::strcmp(key, "deferred") == 0)
         return o.deferred;
     if (std::strcmp(key, "conv_rows") == 0)
-        return kern::conv_rows_enabled();
+        return kern::conv_rows_mode();
+    if (std::strcmp(key, "matmul_rows") == 0)
+        return kern::mm_tile_rows();
     return -1;
 }
 

@@ -181,8 +181,13 @@ bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H
                       int32_t zp_b, const void* tab, const RescaleDev* rs, bool range_safe, void* out, uint32_t* err,
                       hipStream_t stream);
 // Whether int8 3x3 convolutions that fit it run on the row-tile kernel
-// (default) rather than the halo kernel; both are bit-exact.
-void set_conv_rows_enabled(bool on);
+// (mode 1, the default; mode 2: 64-channel workgroups only) rather than the
+// halo kernel (mode 0); all are bit-exact.
+// Rows of A per workgroup of the int8 MATMUL kernel (64 or 128).
+void set_mm_tile_rows(int rows);
+int mm_tile_rows();
+void set_conv_rows_mode(int mode);
+int conv_rows_mode();
 bool conv_rows_enabled();
 // 1x1 stride-1 int8 CONV2D with the fused RESCALE to int8 on the streaming
 // pointwise kernel, for the shapes it takes (conv_i8.hip: K <= 64 a multiple

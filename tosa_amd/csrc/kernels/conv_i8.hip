@@ -147,20 +147,31 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
     // Nonzero when a value fails apply_scale_32's range REQUIRE (one bitwise
     // op per value on the VALU).
     uint32_t bad_bits = 0;
+    // Table entries of channel group tm (4 channels), read one group ahead:
+    // the next group's LDS reads are in flight while this one computes.
+    v4i tq0[2][4], tq1[2][RS ? 4 : 1];
+    auto tab_load = [&](int tm, int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            tq0[slot][i] = s_tab[2 * (cl0 + 4 * tm + i)];
+            if constexpr (RS)
+                tq1[slot][i] = s_tab[2 * (cl0 + 4 * tm + i) + 1];
+        }
+    };
+    tab_load(0, 0);
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
         // One channel group at a time: keeps the scheduler from hoisting every
         // group's table reads (32 registers each) to the top.
         __builtin_amdgcn_sched_barrier(0);
-        v4i t0[4], t1[4];
+        if (tm + 1 < TM)
+            tab_load(tm + 1, (tm + 1) & 1);
+        const v4i* const t0 = tq0[tm & 1];
+        const v4i* const t1 = tq1[tm & 1];
         int32_t hi[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            t0[i] = s_tab[2 * (cl0 + 4 * tm + i)];
-            if constexpr (RS)
-                t1[i] = s_tab[2 * (cl0 + 4 * tm + i) + 1];
+        for (int i = 0; i < 4; i++)
             hi[i] = ~t0[i].z;
-        }
         // The group's residual constants (words 0-18 of each channel).
         int32_t rq[4][RES ? 20 : 1];
         if constexpr (RES) {
@@ -522,21 +533,57 @@ __global__ void __launch_bounds__(256, 2) conv_i8_kernel(ConvI8Args Ain)
     }
 }
 
+// A direct 16-byte global->LDS load (global_load_lds_dwordx4: lane l writes
+// LDS byte address `l` + 16 l, `l` wave-uniform). Issued through inline
+// assembly: LLVM's wait-count pass counts a builtin LDS DMA in flight as an
+// out-of-order LDS event and then makes every LDS read wait for all earlier
+// ones (lgkmcnt(0)), which serialises the fragment prefetch. The callers wait
+// for these loads themselves (s_waitcnt vmcnt(0) and a barrier) before
+// reading what they fill.
+__device__ __forceinline__ void dma16(const void* g, const void* l)
+{
+    const uint32_t la = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((const lvoid*)l)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(la) : "memory", "m0");
+}
+
+typedef __attribute__((address_space(3))) v2i lv2i;
+// Transposing 8-byte LDS read: in each group of 16 lanes, lane i receives
+// byte i % 8 of the 8-byte pieces addressed by lanes 2 j + i / 8 (j = 0..7),
+// as byte j.
+__device__ __forceinline__ v2i ldtr8(const uint8_t* p)
+{
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lv2i*)((const lvoid*)p));
+}
+
 // ---------------------------------------------------------------------------
 // Batched int8 MATMUL with B in its own [C][W] layout
 // ---------------------------------------------------------------------------
 // D[h][w] = sum_c (a[h][c] - za)(b[c][w] - zb) for every batch, in one
-// kernel: the B tile of each stage (KC rows of c, 128 columns w) is loaded as
-// 16-byte row pieces and transposed in registers (4 x 4 byte blocks with
-// v_perm_b32) into LDS rows of c bytes per column, the A operand of the same
-// v_mfma_i32_16x16x64_i8 tiling as conv_i8_kernel (columns = its channels,
-// rows of A = its pixels). The zero-point terms come from the staged bytes:
-// -za sum_c b[c][w] (column sums of the transposed dwords, folded into the
-// tile's table entries before the epilogue) and -zb sum_c a[h][c] (row sums,
-// the epilogue's per-pixel term). The table holds the bias-free additive
-// constant K za zb and the RESCALE parameters, independent of B's values.
-// Two register sets keep the loads of two stages ahead in flight; two
-// workgroups share a CU.
+// kernel, on the v_mfma_i32_16x16x64_i8 tiling of conv_i8_kernel (columns w
+// = its channels, rows h = its pixels): 128 columns x 32 WP rows per
+// workgroup, 2 x WP waves of 64 x 32. Both operands go to LDS with direct
+// global->LDS loads (wave-uniform base, per-lane 32-bit offsets), 128-byte K
+// stages in a ring of three buffers with the loads of two in flight; the
+// ring is unrolled so that every LDS address is a register plus an
+// immediate.
+// * A stage: 1 KB block (rb, ks) holds rows 16 rb .. 16 rb + 15, bytes
+//   64 ks .. 64 ks + 63, lane l = 16 g + j of the block holding row 16 rb + j,
+//   bytes 64 ks + 16 g .. + 15: a 16-row fragment is one contiguous read.
+// * B stage: B's rows as they lie (row k = 128 bytes of columns, 8-byte
+//   piece p stored at p ^ bsw(k)); a column fragment is read with
+//   ds_read_b64_tr_b8: lane t of a 16-lane group addresses row kb + t / 2,
+//   columns c0 + 8 (t % 2) .. + 7, so lane i receives column c0 + i of rows
+//   kb .. kb + 7. The swizzle puts the 16 rows and two pieces that a half
+//   wave reads in distinct banks.
+// The zero-point terms: -za sum_c b[c][w] from one more MFMA per column
+// fragment, against a fragment of za bytes (its result has the
+// accumulators' layout and is subtracted from them), and -zb sum_c a[h][c]
+// from the row fragments (v_dot4, the waves that read the same fragments
+// taking one tn block each; the epilogue's per-pixel term). The table holds
+// the additive constant K za zb and the RESCALE parameters, independent of
+// B's values. Lane (g, j) of a wave ends with the channels 16 tm + 4 g + i
+// of its columns; an exchange through LDS regroups them to the 16
+// consecutive channels per lane the shared epilogue stores.
 struct MatmulI8Args {
     const int8_t* a;  // [batch][H][C]
     const int8_t* b;  // [batch][C][W]
@@ -547,29 +594,59 @@ struct MatmulI8Args {
     EpiArgs E;  // out [batch][H][W]; E.zp_w is B's zero point
 };
 
-template <int OB, bool RS, bool ZA, bool ZB, bool RC>
-__global__ void __launch_bounds__(256, 2) matmul_i8_kernel(MatmulI8Args A)
+// 128 columns x 32 WP rows per workgroup of 2 x WP waves; a ring of three
+// stages (a ring of four measured no faster at 128 rows).
+constexpr int MM_BW = 128, MM_KC = 128;  // columns, K bytes per stage
+constexpr int mm_bh(int wp) { return 32 * wp; }
+constexpr int mm_ns(int) { return 3; }
+constexpr int mm_stage(int wp) { return (MM_BW + mm_bh(wp)) * MM_KC; }
+constexpr size_t mm_lds(int wp)
 {
-    constexpr int BW = 128, BH = 64, KC = 128;  // columns, rows, K bytes per stage
-    constexpr int WC = 2, WP = 2;
+    return size_t(mm_ns(wp)) * mm_stage(wp) + 2 * MM_BW * 16 + mm_bh(wp) * 4;
+}
+
+// dma16 with a wave-uniform 64-bit base and a 32-bit per-lane offset (the
+// saddr form): per-stage address steps are then scalar adds.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, const void* l)
+{
+    const uint32_t la = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((const lvoid*)l)));
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(base), "s"(la)
+                 : "memory", "m0");
+}
+
+template <int WP, int OB, bool RS, bool ZA, bool ZB, bool RC>
+__global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Args A)
+{
+    constexpr int BW = MM_BW, BH = mm_bh(WP), KC = MM_KC, NS = mm_ns(WP), STAGE = mm_stage(WP);
+    constexpr int WC = 2, NW = WC * WP;  // waves
     constexpr int TM = BW / WC / 16, TN = BH / WP / 16;
-    constexpr int SB = (BW + BH) * KC;  // LDS bytes per stage
-    // 16-byte chunk c of column row `col` of the transposed tile sits at c ^
-    // swzw(col): bits 4-6 of the column, so that the transposing dword writes
-    // (columns 16 apart across lanes) spread over the banks, with bit 1 folded
-    // into bit 2, so that the fragment reads (columns differing in bits 0, 1,
-    // 4, 5 across 16 lanes) hit 16 distinct bank groups.
-    auto swzw = [](int col) { return ((col >> 4) & 7) ^ (((col >> 1) & 1) << 2); };
+    constexpr int SA = BH * KC;               // A bytes per stage
+    constexpr int NA = BH * KC / 1024 / NW;   // A direct loads per stage and wave
+    constexpr int NB = BW * KC / 1024 / NW;   // B direct loads per stage and wave
+    constexpr int LPS = NA + NB;
+    static_assert((WP == 2 || WP == 4) && TM == 4 && TN == 2 && NA == 2, "tiling");
+    // 8-byte piece p of B row k sits at p ^ bsw(k): even, so 16-byte pairs
+    // stay pairs.
+    auto bsw = [](int k) { return 2 * (((k >> 1) & 3) | (((k >> 4) & 1) << 2)); };
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    v4i* const s_tab = reinterpret_cast<v4i*>(smem + 2 * SB);          // [BW][2]
+    v4i* const s_tab = reinterpret_cast<v4i*>(smem + NS * STAGE);        // [BW][2]
     int32_t* const s_rowsum = reinterpret_cast<int32_t*>(s_tab + 2 * BW);  // [BH]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wave_c0 = (wave / WP) * (BW / WC);
     const int wave_p0 = (wave % WP) * (BH / WP);
+    const int j16 = lane & 15;
+    const int grp = lane >> 4;
+    // The waves that read the same row fragments take the row sums of one tn
+    // block each: register slot ln holds block (ln + rot_p) of the wave's
+    // blocks, so that the sums read slot 0; the exchange before the epilogue
+    // undoes the rotation.
+    const int rot_p = (wave / WP) % TN;
     // Tile t of XCD x is workgroup x + 8 t (workgroups are dealt round-robin
     // to the XCDs), tiles ordered batch, row tile, column tile: an XCD's
     // workgroups share whole batches of A and B in its L2.
@@ -581,71 +658,54 @@ __global__ void __launch_bounds__(256, 2) matmul_i8_kernel(MatmulI8Args A)
     const int8_t* const a = A.a + bz * A.H * A.C;
     const int8_t* const b = A.b + bz * A.C * A.W;
 
-    // A: row ra of the tile, 16-byte chunks ca and ca + 4 of each stage;
-    // rows past H re-read row H - 1 (their outputs are not stored).
-    const int ra = tid >> 2, ca = tid & 3;
-    const int8_t* const asrc = a + int64_t(h0 + ra < A.H ? h0 + ra : A.H - 1) * A.C + 16 * ca;
-    // B: rows 4 kg .. 4 kg + 3 of each stage, columns 16 nc .. 16 nc + 15 of
-    // the tile (a last partial tile re-reads the final 16 columns, which land
-    // in columns that are not stored).
-    const int kg = tid >> 3, nc = tid & 7;
-    const int wcol = w0 + 16 * nc + 16 <= A.W ? w0 + 16 * nc : A.W - 16;
-    const int8_t* const bsrc = b + int64_t(4 * kg) * A.W + wcol;
+    // This thread's table entry (threads below 2 BW), stored to LDS after the
+    // main loop.
+    const int tcol = w0 + ((tid >> 1) & (BW - 1));
+    const v4i tv = A.tab[2 * (tcol < A.W ? tcol : A.W - 1) + (tid & 1)];
 
-    for (int i = tid; i < 2 * BW; i += 256) {
-        const int c = w0 + (i >> 1);
-        s_tab[i] = A.tab[2 * (c < A.W ? c : A.W - 1) + (i & 1)];
+    // Per-lane offsets of the direct loads from the stage's first byte of A
+    // (column k0) and of B (row k0). A rows past H re-read row H - 1; B pieces
+    // past W re-read the last 16 columns (neither is stored).
+    uint32_t aoff[NA], boff[NB];
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+        const int q = wave + NW * i;  // A block: rows 16 (q / 2) .., bytes 64 (q % 2) ..
+        const int r = h0 + 16 * (q >> 1) + j16;
+        aoff[i] = uint32_t(r < A.H ? r : A.H - 1) * uint32_t(A.C) + 16 * grp + 64 * (q & 1);
     }
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int q = wave + NW * i;  // B rows 8 q .. 8 q + 7
+        const int k = 8 * q + (lane >> 3);
+        const int col = w0 + 8 * ((2 * (lane & 7)) ^ bsw(k));
+        boff[i] = uint32_t(k) * uint32_t(A.W) + uint32_t(col + 16 <= A.W ? col : A.W - 16);
+    }
+    auto issue = [&](int st, auto bufc) {
+        constexpr int BUF = decltype(bufc)::value;
+        uint8_t* const dst = smem + BUF * STAGE;
+        const int8_t* const ab = a + st * KC;
+        const int8_t* const bb = b + int64_t(st * KC) * A.W;
+#pragma unroll
+        for (int i = 0; i < NA; i++)
+            dma16s(ab, aoff[i], dst + (wave + NW * i) * 1024);
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+            dma16s(bb, boff[i], dst + SA + (wave + NW * i) * 1024);
+    };
 
-    v4u av[2][2], bv[2][4];
-    auto load = [&](v4u(&ar)[2], v4u(&br)[4], int k0) {
-        ar[0] = ld16(asrc + k0);
-        ar[1] = ld16(asrc + k0 + 64);
+    // LDS read offsets within a stage: B column fragments (rows 64 ks + 8 half
+    // further on, where the swizzle is the same), A row fragments (ks blocks
+    // 1 KB further on).
+    uint32_t troff[TM], aroff[TN];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            br[i] = ld16(bsrc + int64_t(k0 + i) * A.W);
-    };
-    int32_t csum[16];  // column sums of b over this thread's rows (ZA)
-    int32_t rsum = 0;  // row sum of a over this thread's chunks (ZB)
+    for (int lt = 0; lt < TM; lt++) {
+        const int p = ((wave_c0 + 16 * lt) >> 3) + (j16 & 1);
+        const int k = 16 * grp + (j16 >> 1);
+        troff[lt] = uint32_t(SA + k * BW + ((p ^ bsw(k)) << 3));
+    }
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-        csum[i] = 0;
-    auto store = [&](const v4u(&ar)[2], const v4u(&br)[4], int buf) {
-        uint8_t* const sW = smem + buf * SB;
-        uint8_t* const sX = sW + BW * KC;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = ca + 4 * i;
-            *reinterpret_cast<v4u*>(sX + ra * KC + ((c ^ swz<KC>(ra)) << 4)) = ar[i];
-            if constexpr (ZB) {
-                rsum = __builtin_amdgcn_sdot4(int(ar[i].x), 0x01010101, rsum, false);
-                rsum = __builtin_amdgcn_sdot4(int(ar[i].y), 0x01010101, rsum, false);
-                rsum = __builtin_amdgcn_sdot4(int(ar[i].z), 0x01010101, rsum, false);
-                rsum = __builtin_amdgcn_sdot4(int(ar[i].w), 0x01010101, rsum, false);
-            }
-        }
-        // Dword j of the four rows holds columns 4 j .. 4 j + 3; the 4 x 4
-        // byte transpose gives each column its four consecutive k bytes
-        // (v_perm_b32: selector bytes 0-3 pick the second operand, 4-7 the
-        // first).
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t d0 = br[0][j], d1 = br[1][j], d2 = br[2][j], d3 = br[3][j];
-            const uint32_t t0 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);
-            const uint32_t t1 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);
-            const uint32_t t2 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
-            const uint32_t t3 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
-            const uint32_t e[4] = {__builtin_amdgcn_perm(t2, t0, 0x05040100u), __builtin_amdgcn_perm(t2, t0, 0x07060302u),
-                                   __builtin_amdgcn_perm(t3, t1, 0x05040100u), __builtin_amdgcn_perm(t3, t1, 0x07060302u)};
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const int col = 16 * nc + 4 * j + m;
-                *reinterpret_cast<uint32_t*>(sW + col * KC + (((kg >> 2) ^ swzw(col)) << 4) + 4 * (kg & 3)) = e[m];
-                if constexpr (ZA)
-                    csum[4 * j + m] = __builtin_amdgcn_sdot4(int(e[m]), 0x01010101, csum[4 * j + m], false);
-            }
-        }
-    };
+    for (int lt = 0; lt < TN; lt++)
+        aroff[lt] = uint32_t((((wave_p0 >> 4) + ((lt + rot_p) & (TN - 1))) * 2 * 64 + lane) * 16);
 
     v4i acc[TM][TN];
 #pragma unroll
@@ -653,83 +713,127 @@ __global__ void __launch_bounds__(256, 2) matmul_i8_kernel(MatmulI8Args A)
 #pragma unroll
         for (int j = 0; j < TN; j++)
             acc[i][j] = v4i{0, 0, 0, 0};
-    const int j16 = lane & 15;
-    const int grp = lane >> 4;
-    auto compute = [&](int buf) {
-        const uint8_t* const sW = smem + buf * SB;
-        const uint8_t* const sX = sW + BW * KC;
+    // za sum_k b[k][w] for the channels of acc[tm][.] (ZA): the MFMA of the
+    // column fragments with a fragment of za bytes leaves it in acc's layout.
+    v4i zcs[ZA ? TM : 1];
+#pragma unroll
+    for (int i = 0; i < (ZA ? TM : 1); i++)
+        zcs[i] = v4i{0, 0, 0, 0};
+    const int32_t za4 = int32_t(uint32_t(A.zp_a & 0xff) * 0x01010101u);
+    const v4i zaf = v4i{za4, za4, za4, za4};
+    int32_t rsum = 0;  // row sum of register slot 0 (ZB)
+
+    auto compute = [&](auto bufc) {
+        constexpr int BUF = decltype(bufc)::value;
+        const uint8_t* const sbase = smem + BUF * STAGE;
 #pragma unroll
         for (int ks = 0; ks < KC / 64; ks++) {
-            const int c = ks * 4 + grp;
             v4i af[TM], bf[TN];
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++) {
-                const int row = wave_c0 + (j16 >> 2) * (4 * TM) + 4 * tm + (j16 & 3);
-                af[tm] = *reinterpret_cast<const v4i*>(sW + row * KC + ((c ^ swzw(row)) << 4));
+            for (int lt = 0; lt < TM; lt++) {
+                const v2i h0v = ldtr8(sbase + troff[lt] + (64 * ks) * BW);
+                const v2i h1v = ldtr8(sbase + troff[lt] + (64 * ks + 8) * BW);
+                af[lt] = v4i{h0v.x, h0v.y, h1v.x, h1v.y};
             }
 #pragma unroll
-            for (int tn = 0; tn < TN; tn++) {
-                const int row = wave_p0 + 16 * tn + j16;
-                bf[tn] = *reinterpret_cast<const v4i*>(sX + row * KC + ((c ^ swz<KC>(row)) << 4));
+            for (int lt = 0; lt < TN; lt++)
+                bf[lt] = *reinterpret_cast<const v4i*>(sbase + aroff[lt] + ks * 1024);
+#pragma unroll
+            for (int lt = 0; lt < TM; lt++)
+#pragma unroll
+                for (int ln = 0; ln < TN; ln++)
+                    acc[lt][ln] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[lt], bf[ln], acc[lt][ln], 0, 0, 0);
+            if constexpr (ZA) {
+#pragma unroll
+                for (int lt = 0; lt < TM; lt++)
+                    zcs[lt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[lt], zaf, zcs[lt], 0, 0, 0);
             }
+            if constexpr (ZB) {
 #pragma unroll
-            for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-                for (int tn = 0; tn < TN; tn++)
-                    acc[tm][tn] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+                for (int d = 0; d < 4; d++)
+                    rsum = __builtin_amdgcn_sdot4(bf[0][d], 0x01010101, rsum, false);
+            }
         }
     };
 
-    // Stage s computes from LDS buffer s % 2; the loads of stage s + 2 are
-    // issued into the register set stage s came from, and stage s + 1's
-    // registers are written to the other buffer before the barrier.
     const int nst = A.C / KC;
-    load(av[0], bv[0], 0);
+    using std::integral_constant;
+    // Stage st of the loop below: wait for its loads (vmcnt(N): at most N of
+    // this wave's loads outstanding, those of the next stage already issued;
+    // gfx9 s_waitcnt: vmcnt in bits 3-0 and 15-14, expcnt 6-4 and lgkmcnt
+    // 11-8 left at their maxima), meet at the barrier (every wave's loads of
+    // stage st have landed, and every wave is done with the buffer that stage
+    // st + NS - 1 overwrites: stage st - 1's), issue stage st + NS - 1 and
+    // compute from buffer st % NS.
+    auto step = [&](int st, auto bufc) {
+        constexpr int BUF = decltype(bufc)::value;
+        const int later = nst - 1 - st < NS - 2 ? nst - 1 - st : NS - 2;
+        if (later >= 2)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LPS));
+        else if (later == 1)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | LPS);
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (st + NS - 1 < nst)
+            issue(st + NS - 1, integral_constant<int, (BUF + NS - 1) % NS>{});
+        compute(bufc);
+    };
+    static_assert((NS == 3 || NS == 4) && 2 * LPS < 16, "ring of three or four buffers");
+    issue(0, integral_constant<int, 0>{});
     if (nst > 1)
-        load(av[1], bv[1], KC);
-    store(av[0], bv[0], 0);
-    __syncthreads();
-    for (int s = 0; s < nst; s += 2) {
-        if (s + 2 < nst)
-            load(av[0], bv[0], (s + 2) * KC);
-        compute(0);
-        if (s + 1 < nst)
-            store(av[1], bv[1], 1);
-        __syncthreads();
-        if (s + 1 >= nst)
-            break;
-        if (s + 3 < nst)
-            load(av[1], bv[1], (s + 3) * KC);
-        compute(1);
-        if (s + 2 < nst)
-            store(av[0], bv[0], 0);
-        __syncthreads();
+        issue(1, integral_constant<int, 1>{});
+    if constexpr (NS == 4)
+        if (nst > 2)
+            issue(2, integral_constant<int, 2>{});
+    for (int st = 0; st < nst; st += NS) {
+        step(st, integral_constant<int, 0>{});
+        if (st + 1 < nst)
+            step(st + 1, integral_constant<int, 1>{});
+        if (st + 2 < nst)
+            step(st + 2, integral_constant<int, 2>{});
+        if constexpr (NS == 4)
+            if (st + 3 < nst)
+                step(st + 3, integral_constant<int, 3>{});
     }
+    __syncthreads();  // every wave is done with the ring
 
-    // ---- zero-point terms --------------------------------------------------
+    // ---- zero-point sums, table, channel regrouping ------------------------
+    if (tid < 2 * BW)
+        s_tab[tid] = tv;
     if constexpr (ZA) {
-        // Column sums: 32 row groups x 128 columns, reduced by one thread per
-        // column into its table entry: add -= za sum_c b[c][w].
-        int32_t* const s_cs = reinterpret_cast<int32_t*>(smem);
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            s_cs[kg * BW + 16 * nc + i] = csum[i];
-        __syncthreads();
-        if (tid < BW) {
-            int32_t t = 0;
-            for (int g = 0; g < 32; g++)
-                t += s_cs[g * BW + tid];
-            s_tab[2 * tid].x = int32_t(uint32_t(s_tab[2 * tid].x) - uint32_t(A.zp_a) * uint32_t(t));
-        }
+        for (int lt = 0; lt < TM; lt++)
+#pragma unroll
+            for (int ln = 0; ln < TN; ln++)
+                acc[lt][ln] = v4i(v4u(acc[lt][ln]) - v4u(zcs[lt]));
     }
     if constexpr (ZB) {
-        rsum += __shfl_xor(rsum, 1);
-        rsum += __shfl_xor(rsum, 2);
-        if (ca == 0)
-            s_rowsum[ra] = rsum;
+        int32_t v = rsum;
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (grp == 0)
+            s_rowsum[wave_p0 + 16 * rot_p + j16] = v;
     }
-    if constexpr (ZA || ZB)
-        __syncthreads();
+    // Register slot (lt, ln) of lane (g, j) holds channels 16 tm + 4 g + i of
+    // block tm = lt, tn = (ln + rot_p) % TN; the epilogue takes
+    // acc[tm][tn] with channels 16 g + 4 tm + i: exchange through this wave's
+    // 8 KB of the ring.
+    {
+        uint8_t* const xw = smem + wave * (TM * TN * 64 * 16);
+        auto slot = [&](int tm, int tn, int g) { return xw + (((tn * TM + tm) * 4 + g) * 16 + j16) * 16; };
+#pragma unroll
+        for (int lt = 0; lt < TM; lt++)
+#pragma unroll
+            for (int ln = 0; ln < TN; ln++)
+                *reinterpret_cast<v4i*>(slot(lt, (ln + rot_p) & (TN - 1), grp)) = acc[lt][ln];
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+                acc[tm][tn] = *reinterpret_cast<const v4i*>(slot(grp, tn, tm));
+    }
+    __syncthreads();
 
     auto pixel = [&](int p) { return h0 + p < A.H ? int(bz * A.H + h0 + p) : -1; };
     epilogue<TM, TN, OB, RS, ZB, RC>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, w0, wave_p0, j16, A.E, pixel);
@@ -1088,19 +1192,6 @@ struct Halo32Args {
 // tiles each.
 constexpr int h32_bp(int pg, int tb) { return pg * 32 * tb; }
 constexpr int H32_BP_MAX = h32_bp(8, 2);
-
-// A direct 16-byte global->LDS load (global_load_lds_dwordx4: lane l writes
-// LDS byte address `l` + 16 l, `l` wave-uniform). Issued through inline
-// assembly: LLVM's wait-count pass counts a builtin LDS DMA in flight as an
-// out-of-order LDS event and then makes every LDS read wait for all earlier
-// ones (lgkmcnt(0)), which serialises the fragment prefetch. The callers wait
-// for these loads themselves (s_waitcnt vmcnt(0) and a barrier) before
-// reading what they fill.
-__device__ __forceinline__ void dma16(const void* g, const void* l)
-{
-    const uint32_t la = __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((const lvoid*)l)));
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(la) : "memory", "m0");
-}
 
 // Weight row of MFMA row r (see above).
 __device__ __forceinline__ int h32_row_channel(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
@@ -1614,7 +1705,9 @@ __global__ void __launch_bounds__(BC / 64 * PG * 64, 2) conv_i8_halo32_kernel(Ha
 // pos stored at chunk c ^ ((pos >> 1) & 7), so that 16 consecutive
 // positions reading one chunk hit 16 distinct bank groups) is one LDS image
 // loaded by all eight waves, positions outside the image from the
-// zero-point fill; the consumers stage the epilogue table through LDS.
+// zero-point fill. Only the rows of the first phase are waited for before
+// it starts; the others are loaded behind the weights and stored while it
+// computes. The consumers stage the epilogue table through LDS.
 // ---------------------------------------------------------------------------
 struct RowsArgs {
     const int8_t* x;
@@ -1650,7 +1743,6 @@ __global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
     constexpr int HWP = ROWS_HWP;
     constexpr int HR = RG * RW + 2;
     constexpr int SLOTS = HR * HWP * SL;  // 16-byte halo slots
-    constexpr int NI = (SLOTS + 511) / 512;
     constexpr int HBYTES = SLOTS * 16;
     constexpr int ROWB = HWP * PB;
     constexpr int XW = 2 * 4096;  // transfer bytes per producer wave and buffer (two rows)
@@ -1685,32 +1777,61 @@ __global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
     const int rot = tile & (Q - 1);
     auto chunk = [&](int q) { return (q + rot) & (Q - 1); };
 
-    // Halo slot s = 512 i + tid: chunk s % SL of position (s / SL) % HWP of
-    // halo row s / (SL HWP).
-    v4i hv[NI];
-    auto halo_load = [&]() {
+    // The halo is loaded in two parts: first the rows that each producer's
+    // first phase reads (rows RW g .. RW g + 3 of row group g), then, behind
+    // the weights, the other rows, which land in LDS while the first phase
+    // computes. Slot o of a part (o = 512 i + tid) is chunk o % SL of
+    // position (o / SL) % HWP of the part's row o / (SL HWP).
+    constexpr int EROWS = 4 * RG;
+    constexpr int ESLOTS = EROWS * HWP * SL;
+    constexpr int LSLOTS = SLOTS - ESLOTS;
+    static_assert(ESLOTS % 512 == 0, "whole early slots per thread");
+    constexpr int NE = ESLOTS / 512;
+    constexpr int NL = (LSLOTS + 511) / 512;
+    // Halo row of the k-th row in load order: early rows RW g + 0..3, then
+    // RW g + 4..6 of the groups before the last and the last group's rows
+    // from RW (RG - 1) + 4 to the end.
+    auto row_of = [](int k) {
+        if (k < EROWS)
+            return (k >> 2) * RW + (k & 3);
+        k -= EROWS;
+        const int g = k / 3;
+        return g < RG - 1 ? g * RW + 4 + (k - 3 * g) : (RG - 1) * RW + 4 + (k - 3 * (RG - 1));
+    };
+    v4i hv_e[NE], hv_l[NL];
+    int ho_e[NE], ho_l[NL];  // LDS byte offsets
+    auto halo_load = [&](auto latec, v4i* hv, int* ho) {
+        constexpr bool LATE = decltype(latec)::value;
+        constexpr int NS = LATE ? LSLOTS : ESLOTS;
+        constexpr int NN = LATE ? NL : NE;
         const int8_t* const xi = A.x + int64_t(img) * A.IH * A.IW * A.IC;
 #pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const int sl = 512 * i + tid;
-            if (512 * i + 64 * wave < SLOTS) {
-                const int hp = sl / SL;
-                const int hr = hp / HWP;
+        for (int i = 0; i < NN; i++) {
+            const int o = 512 * i + tid;
+            if (512 * i + 64 * wave < NS) {
+                const int hp = o / SL;
+                const int hr = row_of(hp / HWP + (LATE ? EROWS : 0));
                 const int pos = hp % HWP;
-                const int c = (sl % SL) ^ ((pos >> 1) % SL);
+                const int c = (o % SL) ^ ((pos >> 1) % SL);
                 const int iy = oy0 - A.pt + hr;
                 const int ix = pos - A.pl;
-                const bool ok = hr < HR && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
+                const bool ok = o < NS && unsigned(iy) < unsigned(A.IH) && unsigned(ix) < unsigned(A.IW);
+                ho[i] = ((hr * HWP + pos) * SL + o % SL) * 16;
                 hv[i] = *reinterpret_cast<const v4i*>(ok ? xi + (int64_t(iy) * A.IW + ix) * A.IC + 16 * c : A.zfill);
             }
         }
     };
-    auto halo_store = [&]() {
+    auto halo_store = [&](auto latec, const v4i* hv, const int* ho) {
+        constexpr bool LATE = decltype(latec)::value;
+        constexpr int NS = LATE ? LSLOTS : ESLOTS;
+        constexpr int NN = LATE ? NL : NE;
 #pragma unroll
-        for (int i = 0; i < NI; i++)
-            if (512 * i + 64 * wave < SLOTS && 512 * i + tid < SLOTS)
-                *reinterpret_cast<v4i*>(halo + (512 * i + tid) * 16) = hv[i];
+        for (int i = 0; i < NN; i++)
+            if (512 * i + 64 * wave < NS && 512 * i + tid < NS)
+                *reinterpret_cast<v4i*>(halo + ho[i]) = hv[i];
     };
+    using BF = std::integral_constant<bool, false>;
+    using BT = std::integral_constant<bool, true>;
 
     using std::integral_constant;
     using I0 = integral_constant<int, 0>;
@@ -1721,16 +1842,10 @@ __global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
     static_assert(RW == 7, "phases of 2, 2, 2 and 1 rows");
 
     auto producer = [&]() {
-        halo_load();
-        v4i aw[Q][9];  // chunk q, tap t at ((block Q + chunk(q)) 9 + t) KB
-        {
-            const int8_t* const wsrc = A.wp + int64_t(nw >> 5) * (Q * 9 * 1024) + lane * 16;
-#pragma unroll
-            for (int q = 0; q < Q; q++)
-#pragma unroll
-                for (int t = 0; t < 9; t++)
-                    aw[q][t] = *reinterpret_cast<const v4i*>(wsrc + (chunk(q) * 9 + t) * 1024);
-        }
+        // Loads in the order of first use: the early halo rows, the
+        // accumulators' constants, the weights in the order the first phase's
+        // steps take them, the late halo rows.
+        halo_load(BF{}, hv_e, ho_e);
         v16i init;  // the additive constants of this lane's channels nw + 16 h + i
         {
             const v4i* adds =
@@ -1744,7 +1859,19 @@ __global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
                 init[4 * k + 3] = v.w;
             }
         }
-        halo_store();
+        v4i aw[Q][9];  // chunk q, tap t at ((block Q + chunk(q)) 9 + t) KB
+        {
+            const int8_t* const wsrc = A.wp + int64_t(nw >> 5) * (Q * 9 * 1024) + lane * 16;
+#pragma unroll
+            for (int q = 0; q < Q; q++)
+#pragma unroll
+                for (int kx = 0; kx < 3; kx++)
+#pragma unroll
+                    for (int ky = 0; ky < 3; ky++)
+                        aw[q][3 * ky + kx] = *reinterpret_cast<const v4i*>(wsrc + (chunk(q) * 9 + 3 * ky + kx) * 1024);
+        }
+        halo_load(BT{}, hv_l, ho_l);
+        halo_store(BF{}, hv_e, ho_e);
         __syncthreads();
 
         // Byte offsets of this lane's B fragments within a halo row: position
@@ -1809,6 +1936,7 @@ __global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
                         v4i{acc[r][4 * k], acc[r][4 * k + 1], acc[r][4 * k + 2], acc[r][4 * k + 3]};
         };
         phase(I0{}, I2{}, I0{});
+        halo_store(BT{}, hv_l, ho_l);
         __syncthreads();
         phase(I2{}, I2{}, I1{});
         __syncthreads();
@@ -1819,15 +1947,19 @@ __global__ void __launch_bounds__(512, 1) conv_i8_rows_kernel(RowsArgs A)
     };
 
     auto consumer = [&]() {
-        halo_load();
+        halo_load(BF{}, hv_e, ho_e);
         const int ctid = tid - 256;
         v4i tv = v4i{0, 0, 0, 0};
         if (ctid < 2 * 32 * CB)
             tv = A.tab[2 * n0 + ctid];
-        halo_store();
+        halo_store(BF{}, hv_e, ho_e);
         if (ctid < 2 * 32 * CB)
             s_tab[ctid] = tv;
         __syncthreads();
+        // The consumers' share of the late rows, in LDS before the second
+        // barrier.
+        halo_load(BT{}, hv_l, ho_l);
+        halo_store(BT{}, hv_l, ho_l);
         // Table entries of this lane's channels nw + 16 h + j.
         v4i t0[16], t1[16];
 #pragma unroll
@@ -2954,9 +3086,14 @@ void launch_halo32_epi(const Halo32Args& a, unsigned blocks, size_t lds, int ob,
 
 namespace {
 std::atomic<int> g_conv_rows{1};
+std::atomic<int> g_mm_rows{128};
 }  // namespace
 
-void set_conv_rows_enabled(bool on) { g_conv_rows.store(on ? 1 : 0); }
+void set_mm_tile_rows(int rows) { g_mm_rows.store(rows == 64 ? 64 : 128); }
+int mm_tile_rows() { return g_mm_rows.load(); }
+
+void set_conv_rows_mode(int mode) { g_conv_rows.store(mode == 2 || mode == 4 ? mode : mode != 0); }
+int conv_rows_mode() { return g_conv_rows.load(); }
 bool conv_rows_enabled() { return g_conv_rows.load() != 0; }
 
 // Compute units of the current device (workgroups of the 32x32 halo kernel
@@ -3090,7 +3227,7 @@ bool rows_plan(const ConvI8Desc& d, RowsArgs& a, int& cb, size_t& lds, unsigned&
         d.dx != 1 || d.zp_w != 0 || d.ic != 128 || d.ow < 17 || d.ow > ROWS_HWP - 2 || d.oc % 64 != 0 ||
         d.batch != 1)
         return false;
-    cb = d.oc % 128 == 0 ? 4 : 2;
+    cb = d.oc % 128 == 0 && conv_rows_mode() != 2 ? 4 : 2;
     const int rows = 4 / cb * ROWS_RW;
     a.x = d.x;
     a.wp = d.wpack;
@@ -3254,19 +3391,32 @@ bool matmul_i8_direct_applies(int32_t C, int32_t W, const void* a, const void* b
 
 namespace {
 template <int OB, bool RS, bool ZA, bool ZB, bool RC>
-void launch_mm(const MatmulI8Args& a, int32_t batch, hipStream_t s)
+void launch_mm(const MatmulI8Args& a, int32_t batch, int rows, hipStream_t s)
 {
-    constexpr size_t lds = 2 * (128 + 64) * 128 + 2 * 128 * 16 + 64 * 4;
-    hipLaunchKernelGGL((matmul_i8_kernel<OB, RS, ZA, ZB, RC>), dim3(unsigned(int64_t(a.HT) * a.WT * batch)), dim3(256),
-                       lds, s, a);
+    auto go = [&](auto wpc) {
+        constexpr int WP = decltype(wpc)::value;
+        auto kfn = matmul_i8_kernel<WP, OB, RS, ZA, ZB, RC>;
+        static bool attr = [&]() {
+            hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(mm_lds(WP))),
+                      "matmul_i8 LDS size");
+            return true;
+        }();
+        (void)attr;
+        hipLaunchKernelGGL(kfn, dim3(unsigned(int64_t(a.HT) * a.WT * batch)), dim3(128 * WP), mm_lds(WP), s, a);
+    };
+    if (rows == mm_bh(4))
+        go(std::integral_constant<int, 4>{});
+    else
+        go(std::integral_constant<int, 2>{});
 }
 template <int OB, bool RS, bool RC>
-void launch_mm_zp(const MatmulI8Args& a, int32_t batch, bool za, bool zb, hipStream_t s)
+void launch_mm_zp(const MatmulI8Args& a, int32_t batch, int rows, bool za, bool zb, hipStream_t s)
 {
     if (za)
-        zb ? launch_mm<OB, RS, true, true, RC>(a, batch, s) : launch_mm<OB, RS, true, false, RC>(a, batch, s);
+        zb ? launch_mm<OB, RS, true, true, RC>(a, batch, rows, s) : launch_mm<OB, RS, true, false, RC>(a, batch, rows, s);
     else
-        zb ? launch_mm<OB, RS, false, true, RC>(a, batch, s) : launch_mm<OB, RS, false, false, RC>(a, batch, s);
+        zb ? launch_mm<OB, RS, false, true, RC>(a, batch, rows, s) : launch_mm<OB, RS, false, false, RC>(a, batch, rows, s);
 }
 }  // namespace
 
@@ -3274,7 +3424,9 @@ bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H
                       int32_t zp_b, const void* tab, const RescaleDev* rs, bool range_safe, void* out, uint32_t* err,
                       hipStream_t stream)
 {
-    if (!matmul_i8_direct_applies(C, W, a, b) || (rs && !conv_i8_fast_epilogue_ok(*rs)))
+    // The kernel addresses a batch's rows of A with 32-bit offsets.
+    if (!matmul_i8_direct_applies(C, W, a, b) || (rs && !conv_i8_fast_epilogue_ok(*rs)) ||
+        int64_t(H) * C >= (int64_t(1) << 31))
         return false;
     if (int64_t(batch) * H <= 0)
         return true;
@@ -3285,7 +3437,8 @@ bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H
     m.H = H;
     m.C = C;
     m.W = W;
-    m.HT = (H + 63) / 64;
+    const int rows = mm_tile_rows();  // read once: HT and the launch agree
+    m.HT = (H + rows - 1) / rows;
     m.WT = (W + 127) / 128;
     m.batch = batch;
     if (int64_t(m.HT) * m.WT * batch >= (int64_t(1) << 31))
@@ -3305,15 +3458,15 @@ bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H
     }
     const bool za = zp_a != 0, zb = zp_b != 0;
     if (!rs)
-        launch_mm_zp<4, false, false>(m, batch, za, zb, stream);
+        launch_mm_zp<4, false, false>(m, batch, rows, za, zb, stream);
     else if (e.range)
-        ob == 1 ? launch_mm_zp<1, true, true>(m, batch, za, zb, stream)
-                : ob == 2 ? launch_mm_zp<2, true, true>(m, batch, za, zb, stream)
-                          : launch_mm_zp<4, true, true>(m, batch, za, zb, stream);
+        ob == 1 ? launch_mm_zp<1, true, true>(m, batch, rows, za, zb, stream)
+                : ob == 2 ? launch_mm_zp<2, true, true>(m, batch, rows, za, zb, stream)
+                          : launch_mm_zp<4, true, true>(m, batch, rows, za, zb, stream);
     else
-        ob == 1 ? launch_mm_zp<1, true, false>(m, batch, za, zb, stream)
-                : ob == 2 ? launch_mm_zp<2, true, false>(m, batch, za, zb, stream)
-                          : launch_mm_zp<4, true, false>(m, batch, za, zb, stream);
+        ob == 1 ? launch_mm_zp<1, true, false>(m, batch, rows, za, zb, stream)
+                : ob == 2 ? launch_mm_zp<2, true, false>(m, batch, rows, za, zb, stream)
+                          : launch_mm_zp<4, true, false>(m, batch, rows, za, zb, stream);
     return true;
 }
 
