@@ -37,10 +37,18 @@ def sources():
     return sorted(out)
 
 
+# Per-source compiler options. conv_i8.hip: the machine scheduler that
+# interleaves independent chains (the epilogue's per-value RESCALE chains
+# otherwise run one after another through the same registers).
+SOURCE_FLAGS = {
+    "conv_i8.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
+
+
 def _compile(src):
     rel = os.path.relpath(src, CSRC).replace(os.sep, "_")
     obj = os.path.join(BUILD, rel + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
