@@ -9,7 +9,9 @@ RESCALE(y) and RESCALE(skip) to int32, ADD, RESCALE to int8. The cases pick
 what the fold depends on: reductions on the 64- and 128-byte staging paths;
 pixel counts that leave the last tile partial; 16 to 160 channels (24 and 20
 leave a channel tile partial; 18, not a multiple of 4, takes the residual
-kernel instead); y as the
+kernel instead; 128 channels over few and over many pixels, where the
+convolution alone would take a tile without room for the residual stage);
+y as the
 ADD's first or second operand; per-tensor and per-channel parameters, single
 and double rounding, input and output zero points; a final shift below 32
 (apply_scale_32's value-range REQUIRE checked per value: passing, and
@@ -37,6 +39,8 @@ CASES = [
     (1, 9, 13, 576, 96, True, (30, 32), (True, True, True), (True, True, True)),
     (2, 9, 10, 160, 20, False, (38, 44), (True, False, True), (False, True, True)),
     (1, 6, 7, 144, 18, True, (38, 44), (False, False, True), (True, False, True)),
+    (1, 16, 16, 128, 128, False, (38, 44), (True, True, True), (True, False, True)),
+    (2, 128, 128, 64, 128, True, (38, 44), (False, True, True), (True, True, False)),
 ]
 
 

@@ -2853,7 +2853,11 @@ void launch(const ConvI8Args& a, hipStream_t s)
 template <int BC, int BP, int WC, int WP, int KC, bool PW>
 void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s, bool res = false)
 {
-    if constexpr (PW) {
+    // Tiles of at most eight accumulator fragments per wave take the residual
+    // stage: its per-channel constants and skip bytes would make the
+    // sixteen-fragment tiles (128 x 128, 64 x 256) spill registers.
+    constexpr bool RES_OK = PW && (BC / WC / 16) * (BP / WP / 16) <= 8;
+    if constexpr (RES_OK) {
         if (res) {
             // The quantised residual follows an int8 RESCALE (host-checked).
             if (zw)
@@ -2863,6 +2867,8 @@ void launch_epi(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s, bo
             return;
         }
     }
+    if (res)
+        throw std::logic_error("conv_i8: residual stage on a tile without it");
     if (!rs) {
         if (zw)
             launch<BC, BP, WC, WP, KC, PW, 4, false, true>(a, s);
@@ -2907,11 +2913,13 @@ void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s, b
         for (int i = 1; i < 4; i++)
             if (cost[i] < cost[best])
                 best = i;
-        if (best == 0)
+        // The residual stage takes 32 x 256 for the sixteen-fragment tiles
+        // (launch_epi).
+        if (best == 0 && !res)
             launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s, res);
-        else if (best == 1)
+        else if (best == 1 && !res)
             launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
-        else if (best == 2)
+        else if (best <= 2)
             launch_epi<32, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
             launch_epi<16, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
@@ -2922,14 +2930,16 @@ void launch_tile(const ConvI8Args& a, int ob, bool rs, bool zw, hipStream_t s, b
     // give four times the workgroups, whose extra weight re-reads hit L2.
     const int64_t wgs_needed = 2 * int64_t(cu_count());
     auto few = [&](int64_t bc) { return PW && (int64_t(a.M) + 255) / 256 * ((n + bc - 1) / bc) < wgs_needed; };
-    if (w128 <= w32 && w128 <= w16 && n > 64)
+    // The residual stage takes 64 x 64 or 32 x 256 for the sixteen-fragment
+    // tiles (launch_epi).
+    if (w128 <= w32 && w128 <= w16 && n > 64 && !res)
         launch_epi<128, 128, 2, 2, KC, PW>(a, ob, rs, zw, s, res);
-    else if (w64 <= w32 && w64 <= w16 && n > 32) {
+    else if (w64 <= w32 && w64 <= w16 && n > 32 && (few(64) || !res)) {
         if (few(64))
             launch_epi<64, 64, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
             launch_epi<64, 256, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
-    } else if (w32 <= w16 && n > 16) {
+    } else if ((w32 <= w16 || res) && n > 16) {
         if (few(32))
             launch_epi<32, 64, 1, 4, KC, PW>(a, ob, rs, zw, s, res);
         else
