@@ -58,6 +58,9 @@ struct EpiArgs {
     // Some channel's shift is below 32, so apply_scale_32's value-range
     // REQUIRE can fail and is checked (with every shift >= 32 it cannot).
     int32_t range;
+    // The rounding constant does not depend on the value's sign (single
+    // rounding, or no shift above 31): the tiled epilogue skips the select.
+    int32_t one_round;
     // Quantised residual in the epilogue (kernels instantiated with it): the
     // skip tensor (same layout as the output), the input zero points of its
     // two int8 -> int32 RESCALEs, and the final output range (the last
@@ -159,6 +162,10 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
         }
     };
     tab_load(0, 0);
+    // ONE: E.one_round, as a compile-time flag of each copy of the loop (a
+    // branch on the uniform kernel argument picks the copy).
+    auto groups = [&](auto onec) {
+    constexpr bool ONE = decltype(onec)::value;
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
         // One channel group at a time: keeps the scheduler from hoisting every
@@ -213,7 +220,8 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
                     // apply_scale_32's result REQUIRE cannot fail; rp and rn
                     // carry the output zero point (|zp| <= 2^16), so r is
                     // already RESCALE's r + zp, which fits int32 as well.
-                    const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + (x >= 0 ? rp : rn)) >> t0[i].w);
+                    const int64_t rc = ONE ? rp : (x >= 0 ? rp : rn);
+                    const int32_t r = int32_t((int64_t(x) * int64_t(t0[i].y) + rc) >> t0[i].w);
                     // Output range and CLAMP in one step: the CLAMP bounds lie
                     // inside the output type's range, so clamping to the
                     // type and then to [clo, chi] is clamping to [clo, chi].
@@ -263,6 +271,11 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
                 asm volatile("" : "+v"(bad_bits));
         }
     }
+    };
+    if (!RS || E.one_round)
+        groups(std::true_type{});
+    else
+        groups(std::false_type{});
 
 #pragma unroll
     for (int tn = 0; tn < TN; tn++) {
@@ -3464,6 +3477,7 @@ bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H
         e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
         e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
         e.range = rs->min_shift <= 31 && !range_safe;
+        e.one_round = rs->rounding != 3 || rs->max_shift <= 31;
         ob = rs->out_bytes;
     }
     const bool za = zp_a != 0, zb = zp_b != 0;
@@ -3503,6 +3517,7 @@ bool conv_i8_pointwise_stream(const ConvI8Desc& d, const void* tab, const Rescal
     e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
     e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
     e.range = rs->min_shift <= 31 && !d.range_safe;
+    e.one_round = rs->rounding != 3 || rs->max_shift <= 31;
     const bool zw = d.zp_w != 0;
     if (d.ic <= 32) {
         if (zw)
@@ -3564,6 +3579,7 @@ bool conv_i8_stem(const ConvI8Desc& d, const void* tab, const int8_t* wpad, cons
     e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
     e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
     e.range = rs->min_shift <= 31 && !d.range_safe;
+    e.one_round = rs->rounding != 3 || rs->max_shift <= 31;
     const size_t lds = size_t(a.HR) * a.WP * 4;
     if (lds > 64 * 1024)
         return false;
@@ -3758,6 +3774,7 @@ void conv_i8_fast(const ConvI8Desc& d, const void* tab, const RescaleDev* rs, vo
         e.clo = int32_t(rs->has_clamp ? std::max<int64_t>(rs->clamp_lo, rs->lo) : rs->lo);
         e.chi = int32_t(rs->has_clamp ? std::min<int64_t>(rs->clamp_hi, rs->hi) : rs->hi);
         e.range = rs->min_shift <= 31 && !d.range_safe;
+        e.one_round = rs->rounding != 3 || rs->max_shift <= 31;
         ob = rs->out_bytes;
     }
     if (int64_t(d.n) * d.oh * d.ow <= 0 || d.oc <= 0)
