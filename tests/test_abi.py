@@ -144,6 +144,24 @@ def test_options_round_trip():
         T.set_option("no_such_option", 1)
 
 
+@pytest.mark.parametrize("key,default,values", [
+    ("conv_rows", 1, [(0, 0), (2, 2), (4, 1), (7, 1), (1, 1)]),
+    ("matmul_rows", 128, [(64, 64), (128, 128), (100, 128), (0, 128)]),
+])
+def test_kernel_tiling_options(key, default, values):
+    # Process-wide tiling choices: documented values are kept, others map to
+    # the default kind (any nonzero conv_rows value other than 2 is 1;
+    # any matmul_rows value other than 64 is 128).
+    assert T.get_option(key) == default
+    try:
+        for value, kept in values:
+            T.set_option(key, value)
+            assert T.get_option(key) == kept, (value, kept)
+    finally:
+        T.set_option(key, default)
+    assert T.get_option(key) == default
+
+
 def test_interpreter_replans_for_each_input_name_set():
     # One Interpreter, runs alternating between complete and incomplete input
     # sets: the ready queue's starting state is kept per set of input names,

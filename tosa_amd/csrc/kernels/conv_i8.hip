@@ -3115,7 +3115,7 @@ std::atomic<int> g_mm_rows{128};
 void set_mm_tile_rows(int rows) { g_mm_rows.store(rows == 64 ? 64 : 128); }
 int mm_tile_rows() { return g_mm_rows.load(); }
 
-void set_conv_rows_mode(int mode) { g_conv_rows.store(mode == 2 || mode == 4 ? mode : mode != 0); }
+void set_conv_rows_mode(int mode) { g_conv_rows.store(mode == 2 ? 2 : mode != 0); }
 int conv_rows_mode() { return g_conv_rows.load(); }
 bool conv_rows_enabled() { return g_conv_rows.load() != 0; }
 
