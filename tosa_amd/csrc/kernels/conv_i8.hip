@@ -3447,9 +3447,10 @@ bool matmul_i8_direct(const int8_t* a, const int8_t* b, int32_t batch, int32_t H
                       int32_t zp_b, const void* tab, const RescaleDev* rs, bool range_safe, void* out, uint32_t* err,
                       hipStream_t stream)
 {
-    // The kernel addresses a batch's rows of A with 32-bit offsets.
+    // The kernel addresses a batch's rows of A, and a stage's 128 rows of B,
+    // with 32-bit offsets.
     if (!matmul_i8_direct_applies(C, W, a, b) || (rs && !conv_i8_fast_epilogue_ok(*rs)) ||
-        int64_t(H) * C >= (int64_t(1) << 31))
+        int64_t(H) * C >= (int64_t(1) << 31) || int64_t(W) * MM_KC >= (int64_t(1) << 31))
         return false;
     if (int64_t(batch) * H <= 0)
         return true;
