@@ -78,9 +78,11 @@ class Tensor:
                                             ctypes.c_void_p(ptr), nbytes, ctypes.byref(h)))
         return cls(h, keep=keep)
 
-    def __del__(self):
-        if getattr(self, "_owned", False) and self._h and _lib.loaded():
-            lib().tosa_tensor_free(self._h)
+    # The library module is bound as a default argument: at interpreter exit
+    # module globals may already be cleared when the last objects go.
+    def __del__(self, _l=_lib):
+        if getattr(self, "_owned", False) and self._h and _l.loaded():
+            _l.lib().tosa_tensor_free(self._h)
             self._h = None
 
     @property
@@ -137,9 +139,9 @@ class _Hook:
     def _native(self):
         return self._handle
 
-    def __del__(self):
-        if self._handle and not self._borrowed and _lib.loaded():
-            lib().tosa_hook_free(self._handle)
+    def __del__(self, _l=_lib):
+        if self._handle and not self._borrowed and _l.loaded():
+            _l.lib().tosa_hook_free(self._handle)
             self._handle = None
 
 
@@ -317,9 +319,9 @@ class Interpreter:
         check(lib().tosa_graph_from_flatbuffer(buf, len(data), ctypes.byref(h)))
         return cls(h)
 
-    def __del__(self):
-        if getattr(self, "_h", None) and _lib.loaded():
-            lib().tosa_graph_free(self._h)
+    def __del__(self, _l=_lib):
+        if getattr(self, "_h", None) and _l.loaded():
+            _l.lib().tosa_graph_free(self._h)
             self._h = None
 
     def graph(self) -> dict:
