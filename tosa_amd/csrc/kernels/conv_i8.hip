@@ -124,12 +124,16 @@ __device__ __forceinline__ int32_t res_apply(int32_t x, int32_t m, int32_t s, in
 // y' = RESCALE(RESCALE(y - za) + RESCALE(skip - zb)) with the constants of
 // s_res (CONV_I8_RES_WORDS per tile channel: m, s, rp, rn of each of the
 // three RESCALEs, then the last one's value-range bound), and y' is stored.
-template <int TM, int TN, int OB, bool RS, bool ZW, bool RC, bool RES = false, typename PixelMap>
+// CS: tile channels between consecutive channel groups tm of a lane (4: the
+// lane's 4 TM channels are consecutive; 16: groups of 4 consecutive channels
+// 16 apart, each stored on its own).
+template <int TM, int TN, int OB, bool RS, bool ZW, bool RC, bool RES = false, int CS = 4, typename PixelMap>
 __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, const int32_t* s_rowsum, int cl0,
                                          int n0, int wave_p0, int j16, const EpiArgs& E, PixelMap pixel,
                                          const int32_t* s_res = nullptr)
 {
     static_assert(!RES || (RS && OB == 1), "the residual follows an int8 RESCALE");
+    static_assert(CS == 4 || !RES, "the residual stage takes consecutive channels");
     constexpr int WORDS = TM * OB;  // 32-bit words of output per lane and pixel
     const int c0 = n0 + cl0;
     uint32_t res[TN][WORDS];
@@ -156,9 +160,9 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
     auto tab_load = [&](int tm, int slot) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            tq0[slot][i] = s_tab[2 * (cl0 + 4 * tm + i)];
+            tq0[slot][i] = s_tab[2 * (cl0 + CS * tm + i)];
             if constexpr (RS)
-                tq1[slot][i] = s_tab[2 * (cl0 + 4 * tm + i) + 1];
+                tq1[slot][i] = s_tab[2 * (cl0 + CS * tm + i) + 1];
         }
     };
     tab_load(0, 0);
@@ -277,6 +281,46 @@ __device__ __forceinline__ void epilogue(v4i (&acc)[TM][TN], const v4i* s_tab, c
     else
         groups(std::false_type{});
 
+    if constexpr (CS != 4) {
+        // Each channel group on its own: 4 channels, OB words.
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+            const int m = pixel(wave_p0 + 16 * tn + j16);
+            if (m < 0)
+                continue;
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++) {
+                const int cb = c0 + CS * tm;
+                uint8_t* dst = E.out + (int64_t(m) * E.N + cb) * OB;
+                if (cb + 4 <= E.N && (reinterpret_cast<uintptr_t>(dst) % (4 * OB)) == 0) {
+                    if constexpr (OB == 1)
+                        *reinterpret_cast<uint32_t*>(dst) = res[tn][tm];
+                    else if constexpr (OB == 2)
+                        *reinterpret_cast<v2u*>(dst) = v2u{res[tn][2 * tm], res[tn][2 * tm + 1]};
+                    else
+                        *reinterpret_cast<v4u*>(dst) =
+                            v4u{res[tn][4 * tm], res[tn][4 * tm + 1], res[tn][4 * tm + 2], res[tn][4 * tm + 3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (cb + e >= E.N)
+                            continue;
+                        const uint32_t word = res[tn][(4 * tm + e) * OB / 4];
+                        const int sh = 8 * (((4 * tm + e) * OB) % 4);
+                        if constexpr (OB == 1)
+                            dst[e] = uint8_t(word >> sh);
+                        else if constexpr (OB == 2)
+                            reinterpret_cast<uint16_t*>(dst)[e] = uint16_t(word >> sh);
+                        else
+                            reinterpret_cast<uint32_t*>(dst)[e] = word;
+                    }
+                }
+            }
+        }
+        if (bad_bits | res_bad)
+            atomicOr(E.err, DERR_SCALE_RANGE);
+        return;
+    }
 #pragma unroll
     for (int tn = 0; tn < TN; tn++) {
         const int m = pixel(wave_p0 + 16 * tn + j16);
@@ -589,14 +633,12 @@ __device__ __forceinline__ v2i ldtr8(const uint8_t* p)
 //   kb .. kb + 7. The swizzle puts the 16 rows and two pieces that a half
 //   wave reads in distinct banks.
 // The zero-point terms: -za sum_c b[c][w] from one more MFMA per column
-// fragment, against a fragment of za bytes (its result has the
-// accumulators' layout and is subtracted from them), and -zb sum_c a[h][c]
-// from the row fragments (v_dot4, the waves that read the same fragments
-// taking one tn block each; the epilogue's per-pixel term). The table holds
-// the additive constant K za zb and the RESCALE parameters, independent of
-// B's values. Lane (g, j) of a wave ends with the channels 16 tm + 4 g + i
-// of its columns; an exchange through LDS regroups them to the 16
-// consecutive channels per lane the shared epilogue stores.
+// fragment, against a fragment of za bytes, and -zb sum_c a[h][c] from one
+// more MFMA per row fragment, with a fragment of zb bytes; both results have
+// the accumulators' layout and are subtracted from them. The table holds the
+// additive constant K za zb and the RESCALE parameters, independent of B's
+// values. Lane (g, j) of a wave ends with the channels 16 tm + 4 g + i of its
+// columns, which the shared epilogue stores group by group.
 struct MatmulI8Args {
     const int8_t* a;  // [batch][H][C]
     const int8_t* b;  // [batch][C][W]
@@ -615,7 +657,7 @@ constexpr int mm_ns(int) { return 3; }
 constexpr int mm_stage(int wp) { return (MM_BW + mm_bh(wp)) * MM_KC; }
 constexpr size_t mm_lds(int wp)
 {
-    return size_t(mm_ns(wp)) * mm_stage(wp) + 2 * MM_BW * 16 + mm_bh(wp) * 4;
+    return size_t(mm_ns(wp)) * mm_stage(wp) + 2 * MM_BW * 16;
 }
 
 // dma16 with a wave-uniform 64-bit base and a 32-bit per-lane offset (the
@@ -645,8 +687,7 @@ __global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Arg
     auto bsw = [](int k) { return 2 * (((k >> 1) & 3) | (((k >> 4) & 1) << 2)); };
 
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    v4i* const s_tab = reinterpret_cast<v4i*>(smem + NS * STAGE);        // [BW][2]
-    int32_t* const s_rowsum = reinterpret_cast<int32_t*>(s_tab + 2 * BW);  // [BH]
+    v4i* const s_tab = reinterpret_cast<v4i*>(smem + NS * STAGE);  // [BW][2]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -655,11 +696,6 @@ __global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Arg
     const int wave_p0 = (wave % WP) * (BH / WP);
     const int j16 = lane & 15;
     const int grp = lane >> 4;
-    // The waves that read the same row fragments take the row sums of one tn
-    // block each: register slot ln holds block (ln + rot_p) of the wave's
-    // blocks, so that the sums read slot 0; the exchange before the epilogue
-    // undoes the rotation.
-    const int rot_p = (wave / WP) % TN;
     // Tile t of XCD x is workgroup x + 8 t (workgroups are dealt round-robin
     // to the XCDs), tiles ordered batch, row tile, column tile: an XCD's
     // workgroups share whole batches of A and B in its L2.
@@ -718,7 +754,7 @@ __global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Arg
     }
 #pragma unroll
     for (int lt = 0; lt < TN; lt++)
-        aroff[lt] = uint32_t((((wave_p0 >> 4) + ((lt + rot_p) & (TN - 1))) * 2 * 64 + lane) * 16);
+        aroff[lt] = uint32_t((((wave_p0 >> 4) + lt) * 2 * 64 + lane) * 16);
 
     v4i acc[TM][TN];
 #pragma unroll
@@ -726,15 +762,20 @@ __global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Arg
 #pragma unroll
         for (int j = 0; j < TN; j++)
             acc[i][j] = v4i{0, 0, 0, 0};
-    // za sum_k b[k][w] for the channels of acc[tm][.] (ZA): the MFMA of the
-    // column fragments with a fragment of za bytes leaves it in acc's layout.
-    v4i zcs[ZA ? TM : 1];
+    // za sum_k b[k][w] for the channels of acc[tm][.] (ZA) and zb sum_k a[h][k]
+    // for the rows of acc[.][tn] (ZB): the MFMAs of the column fragments with
+    // a fragment of za bytes, and of a fragment of zb bytes with the row
+    // fragments, leave them in acc's layout.
+    v4i zcs[ZA ? TM : 1], zrs[ZB ? TN : 1];
 #pragma unroll
     for (int i = 0; i < (ZA ? TM : 1); i++)
         zcs[i] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < (ZB ? TN : 1); i++)
+        zrs[i] = v4i{0, 0, 0, 0};
     const int32_t za4 = int32_t(uint32_t(A.zp_a & 0xff) * 0x01010101u);
-    const v4i zaf = v4i{za4, za4, za4, za4};
-    int32_t rsum = 0;  // row sum of register slot 0 (ZB)
+    const int32_t zb4 = int32_t(uint32_t(A.E.zp_w & 0xff) * 0x01010101u);
+    const v4i zaf = v4i{za4, za4, za4, za4}, zbf = v4i{zb4, zb4, zb4, zb4};
 
     auto compute = [&](auto bufc) {
         constexpr int BUF = decltype(bufc)::value;
@@ -763,8 +804,8 @@ __global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Arg
             }
             if constexpr (ZB) {
 #pragma unroll
-                for (int d = 0; d < 4; d++)
-                    rsum = __builtin_amdgcn_sdot4(bf[0][d], 0x01010101, rsum, false);
+                for (int ln = 0; ln < TN; ln++)
+                    zrs[ln] = __builtin_amdgcn_mfma_i32_16x16x64_i8(zbf, bf[ln], zrs[ln], 0, 0, 0);
             }
         }
     };
@@ -809,47 +850,27 @@ __global__ void __launch_bounds__(128 * WP, 4 / WP) matmul_i8_kernel(MatmulI8Arg
             if (st + 3 < nst)
                 step(st + 3, integral_constant<int, 3>{});
     }
-    __syncthreads();  // every wave is done with the ring
-
-    // ---- zero-point sums, table, channel regrouping ------------------------
+    // ---- zero-point terms and table --------------------------------------
     if (tid < 2 * BW)
         s_tab[tid] = tv;
-    if constexpr (ZA) {
 #pragma unroll
-        for (int lt = 0; lt < TM; lt++)
+    for (int lt = 0; lt < TM; lt++)
 #pragma unroll
-            for (int ln = 0; ln < TN; ln++)
-                acc[lt][ln] = v4i(v4u(acc[lt][ln]) - v4u(zcs[lt]));
-    }
-    if constexpr (ZB) {
-        int32_t v = rsum;
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
-        if (grp == 0)
-            s_rowsum[wave_p0 + 16 * rot_p + j16] = v;
-    }
-    // Register slot (lt, ln) of lane (g, j) holds channels 16 tm + 4 g + i of
-    // block tm = lt, tn = (ln + rot_p) % TN; the epilogue takes
-    // acc[tm][tn] with channels 16 g + 4 tm + i: exchange through this wave's
-    // 8 KB of the ring.
-    {
-        uint8_t* const xw = smem + wave * (TM * TN * 64 * 16);
-        auto slot = [&](int tm, int tn, int g) { return xw + (((tn * TM + tm) * 4 + g) * 16 + j16) * 16; };
-#pragma unroll
-        for (int lt = 0; lt < TM; lt++)
-#pragma unroll
-            for (int ln = 0; ln < TN; ln++)
-                *reinterpret_cast<v4i*>(slot(lt, (ln + rot_p) & (TN - 1), grp)) = acc[lt][ln];
-#pragma unroll
-        for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-            for (int tn = 0; tn < TN; tn++)
-                acc[tm][tn] = *reinterpret_cast<const v4i*>(slot(grp, tn, tm));
-    }
-    __syncthreads();
+        for (int ln = 0; ln < TN; ln++) {
+            v4u v = v4u(acc[lt][ln]);
+            if constexpr (ZA)
+                v -= v4u(zcs[lt]);
+            if constexpr (ZB)
+                v -= v4u(zrs[ln]);
+            acc[lt][ln] = v4i(v);
+        }
+    __syncthreads();  // the table is in LDS
 
+    // Lane (g, j) holds channels 16 tm + 4 g + i of acc[tm][tn]: the epilogue
+    // stores each group of four on its own.
     auto pixel = [&](int p) { return h0 + p < A.H ? int(bz * A.H + h0 + p) : -1; };
-    epilogue<TM, TN, OB, RS, ZB, RC>(acc, s_tab, s_rowsum, wave_c0 + grp * 4 * TM, w0, wave_p0, j16, A.E, pixel);
+    epilogue<TM, TN, OB, RS, false, RC, false, 16>(acc, s_tab, nullptr, wave_c0 + 4 * grp, w0, wave_p0, j16, A.E,
+                                                    pixel);
 }
 
 // ---------------------------------------------------------------------------
