@@ -227,6 +227,21 @@ tosa_status tosa_conv2d_i8(const int8_t* x, const int64_t x_shape[4], const int8
                            const tosa_rescale_i32* rescale, void* out, int64_t out_shape[4],
                            uint32_t* device_error, void* stream);
 
+/* int8 MATMUL: eval_matmul's integer branch (src/ops/matmul.rs:98-153; the
+ * product loop Dims::run, :80-95) with its shape checks (:112-123). a
+ * [N,H,C] and b [N,C,W] int8, device pointers (16-byte aligned); a_shape
+ * {N, H, C}, b_shape {N, C, W}; a_zp and b_zp int8 values. out receives
+ * [N,H,W]: int32 without `rescale`, else the rescale's output type (one
+ * multiplier/shift pair or W of them); out_shape (may be NULL) the output
+ * shape; with out NULL the call only checks its arguments and fills
+ * out_shape. device_error and stream as for tosa_conv2d_i8. The epilogue
+ * table is rebuilt on every call in workspace from the stream's pool. C must
+ * be a multiple of 128 and W of 16 (TOSA_ERR_UNSUPPORTED_OP otherwise: run
+ * such a MATMUL through a graph). */
+tosa_status tosa_matmul_i8(const int8_t* a, const int64_t a_shape[3], const int8_t* b, const int64_t b_shape[3],
+                           int32_t a_zp, int32_t b_zp, const tosa_rescale_i32* rescale, void* out,
+                           int64_t out_shape[3], uint32_t* device_error, void* stream);
+
 /* No counterpart in the reference: tosa_conv2d_i8 for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc). Same arguments and results, but the

@@ -419,20 +419,42 @@ def conv2d_i8(x_ptr, x_shape, w_ptr, w_shape, bias_ptr, bias_len, input_zp=0, we
     st = (ctypes.c_int32 * 2)(*stride)
     dl = (ctypes.c_int32 * 2)(*dilation)
     os_ = (ctypes.c_int64 * 4)()
-    rs_p, keep = None, []
-    if rescale is not None:
-        m = np.ascontiguousarray(np.asarray(rescale["multiplier"], dtype=np.int32).reshape(-1))
-        sh = np.ascontiguousarray(np.asarray(rescale["shift"], dtype=np.int8).reshape(-1))
-        keep += [m, sh]
-        clamp = rescale.get("clamp")
-        rs = _lib.RescaleI32(m.ctypes.data, sh.ctypes.data, len(m), int(bool(rescale.get("double_round", True))),
-                             DTYPE_CODE[rescale.get("output_dtype", "INT8")], int(rescale.get("output_zp", 0)),
-                             int(clamp is not None), int(clamp[0]) if clamp else 0, int(clamp[1]) if clamp else 0)
-        rs_p = ctypes.pointer(rs)
+    keep = []
+    rs_p = _rescale_arg(rescale, keep)
     fn = lib().tosa_conv2d_i8_noalloc if no_alloc else lib().tosa_conv2d_i8
     check(fn(ctypes.c_void_p(x_ptr), xs, ctypes.c_void_p(w_ptr), ws, ctypes.c_void_p(bias_ptr), int(bias_len),
              int(input_zp), int(weight_zp), pd, st, dl, rs_p, ctypes.c_void_p(out_ptr), os_,
              ctypes.c_void_p(device_error or 0), ctypes.c_void_p(stream or 0)))
+    del keep
+    return tuple(os_)
+
+
+def _rescale_arg(rescale, keep):
+    if rescale is None:
+        return None
+    m = np.ascontiguousarray(np.asarray(rescale["multiplier"], dtype=np.int32).reshape(-1))
+    sh = np.ascontiguousarray(np.asarray(rescale["shift"], dtype=np.int8).reshape(-1))
+    keep += [m, sh]
+    clamp = rescale.get("clamp")
+    rs = _lib.RescaleI32(m.ctypes.data, sh.ctypes.data, len(m), int(bool(rescale.get("double_round", True))),
+                         DTYPE_CODE[rescale.get("output_dtype", "INT8")], int(rescale.get("output_zp", 0)),
+                         int(clamp is not None), int(clamp[0]) if clamp else 0, int(clamp[1]) if clamp else 0)
+    return ctypes.pointer(rs)
+
+
+def matmul_i8(a_ptr, a_shape, b_ptr, b_shape, a_zp=0, b_zp=0, rescale=None, out_ptr=0, device_error=0, stream=0):
+    """Op-level int8 MATMUL on device buffers (tosa_matmul_i8): a [N,H,C] and
+    b [N,C,W] int8, out [N,H,W] (int32, or the rescale's type), given as
+    device addresses; returns the output shape. `rescale` as for conv2d_i8
+    (1 or W multiplier/shift values); `device_error` and `stream` as there."""
+    as_ = (ctypes.c_int64 * 3)(*a_shape)
+    bs = (ctypes.c_int64 * 3)(*b_shape)
+    os_ = (ctypes.c_int64 * 3)()
+    keep = []
+    rs_p = _rescale_arg(rescale, keep)
+    check(lib().tosa_matmul_i8(ctypes.c_void_p(a_ptr), as_, ctypes.c_void_p(b_ptr), bs, int(a_zp), int(b_zp), rs_p,
+                               ctypes.c_void_p(out_ptr), os_, ctypes.c_void_p(device_error or 0),
+                               ctypes.c_void_p(stream or 0)))
     del keep
     return tuple(os_)
 

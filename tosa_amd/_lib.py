@@ -141,6 +141,9 @@ SIGNATURES = {
     "tosa_device_count": (ctypes.c_int, []),
     "tosa_conv2d_i8": (ctypes.c_int, _CONV2D_I8_ARGS),
     "tosa_conv2d_i8_noalloc": (ctypes.c_int, _CONV2D_I8_ARGS),
+    "tosa_matmul_i8": (ctypes.c_int, [P, ctypes.POINTER(ctypes.c_int64), P, ctypes.POINTER(ctypes.c_int64),
+                                      ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(RescaleI32), P,
+                                      ctypes.POINTER(ctypes.c_int64), P, P]),
 }
 
 

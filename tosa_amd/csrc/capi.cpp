@@ -633,6 +633,26 @@ tosa_status tosa_conv2d_i8(const int8_t* x, const int64_t x_shape[4], const int8
     });
 }
 
+tosa_status tosa_matmul_i8(const int8_t* a, const int64_t a_shape[3], const int8_t* b, const int64_t b_shape[3],
+                           int32_t a_zp, int32_t b_zp, const tosa_rescale_i32* rescale, void* out,
+                           int64_t out_shape[3], uint32_t* device_error, void* stream)
+{
+    return guard([&] {
+        MatmulI8OpArgs m;
+        m.a = a;
+        m.a_shape = a_shape;
+        m.b = b;
+        m.b_shape = b_shape;
+        m.a_zp = a_zp;
+        m.b_zp = b_zp;
+        m.rescale = rescale;
+        m.out = out;
+        m.device_error = device_error;
+        m.stream = stream;
+        matmul_i8(m, out_shape);
+    });
+}
+
 tosa_status tosa_conv2d_i8_noalloc(const int8_t* x, const int64_t x_shape[4], const int8_t* w,
                                    const int64_t w_shape[4], const int32_t* bias, int64_t bias_len, int32_t input_zp,
                                    int32_t weight_zp, const int32_t pad[4], const int32_t stride[2],

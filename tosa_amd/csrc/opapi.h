@@ -58,4 +58,20 @@ void conv2d_i8(const ConvI8Args& a, int64_t* out_shape);
 // tosa_conv2d_i8_noalloc: workspace in the per-GPU static scratch array.
 void conv2d_i8_noalloc(const ConvI8Args& a, int64_t* out_shape);
 
+// The arguments of tosa_matmul_i8 (include/tosa_mi355x.h).
+struct MatmulI8OpArgs {
+    const int8_t* a = nullptr;
+    const int64_t* a_shape = nullptr;  // {N, H, C}
+    const int8_t* b = nullptr;
+    const int64_t* b_shape = nullptr;  // {N, C, W}
+    int32_t a_zp = 0, b_zp = 0;
+    const tosa_rescale_i32* rescale = nullptr;
+    void* out = nullptr;
+    uint32_t* device_error = nullptr;
+    void* stream = nullptr;
+};
+// tosa_matmul_i8: workspace (RESCALE words, epilogue table) from the
+// stream's pool.
+void matmul_i8(const MatmulI8OpArgs& a, int64_t* out_shape);
+
 }  // namespace tosa

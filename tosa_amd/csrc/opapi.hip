@@ -105,6 +105,60 @@ void upload_words(const std::vector<int32_t>& words, int32_t* dst, hipStream_t s
     }
 }
 
+// RESCALE (and CLAMP) parameters of an op-level call: eval_rescale's checks
+// for an int32 input with scale32 and input zero point 0
+// (src/ops/type_conv.rs:111-191), apply_scale_32's parameter REQUIRE
+// (src/ops/quant.rs:17-32) when there is any output, CLAMP's bounds
+// (src/ops/elementwise.rs:314-343). `params` receives the multipliers, then
+// the shifts, as int32 words.
+void parse_rescale(const tosa_rescale_i32& r, int64_t oc, int64_t count, RescaleDev& rs, std::vector<int32_t>& params)
+{
+    const std::string RS = "RESCALE";
+    if (!r.multiplier || !r.shift)
+        throw bad_arg(RS + ": null multiplier or shift");
+    if (r.channels != 1 && r.channels != oc)
+        throw invalid(RS, "multiplier and shift must have 1 or " + std::to_string(oc) + " elements");
+    const DType out_t = static_cast<DType>(r.output_dtype);
+    if (out_t != DT_INT8 && out_t != DT_INT16 && out_t != DT_INT32)
+        throw Error(ERR_DTYPE_MISMATCH, RS + ": unsupported types INT32 -> " + dtype_name(out_t));
+    if (out_t == DT_INT8 ? (r.output_zp < -128 || r.output_zp > 127) : r.output_zp != 0)
+        throw invalid(RS, "zero point not allowed for this type");
+    rs.channels = r.channels;
+    rs.per_channel = r.channels > 1 ? 1 : 0;
+    rs.scale32 = 1;
+    rs.rounding = r.double_round ? 3 : 1;
+    rs.in_bits = 32;
+    rs.in_unsigned = 0;
+    rs.in_zp = 0;
+    rs.out_zp = r.output_zp;
+    const int bits = out_t == DT_INT8 ? 8 : out_t == DT_INT16 ? 16 : 32;
+    rs.lo = -(int64_t(1) << (bits - 1));
+    rs.hi = (int64_t(1) << (bits - 1)) - 1;
+    rs.out_bytes = bits / 8;
+    if (r.has_clamp) {
+        if (r.clamp_min < rs.lo || r.clamp_max > rs.hi)
+            throw invalid("CLAMP", "min_val and max_val must be values of the output type");
+        if (r.clamp_max < r.clamp_min)
+            throw invalid("CLAMP", "max_val must not be smaller than min_val");
+        rs.has_clamp = 1;
+        rs.clamp_lo = r.clamp_min;
+        rs.clamp_hi = r.clamp_max;
+    }
+    rs.max_shift = 2;
+    rs.min_shift = 62;
+    params.resize(size_t(2 * r.channels));
+    for (int32_t i = 0; i < r.channels; i++) {
+        const int32_t m = r.multiplier[i], sh = r.shift[i];
+        if (count > 0 && (m < 0 || sh < 2 || sh > 62))
+            throw Error(ERR_GRAPH, "apply_scale_32: invalid multiplier " + std::to_string(m) + " or shift " +
+                                       std::to_string(sh));
+        params[size_t(i)] = m;
+        params[size_t(r.channels + i)] = sh;
+        rs.max_shift = std::max(rs.max_shift, sh);
+        rs.min_shift = std::min(rs.min_shift, sh);
+    }
+}
+
 }  // namespace
 
 ConvI8Call prepare_conv2d_i8(const ConvI8Args& a)
@@ -174,54 +228,10 @@ ConvI8Call prepare_conv2d_i8(const ConvI8Args& a)
                                       "multiple of 16 (1x1 stride 1 unpadded) or of 64 (any other geometry); "
                                       "other convolutions run through a graph");
 
-    if (const tosa_rescale_i32* r = a.rescale) {
-        const std::string RS = "RESCALE";
-        if (!r->multiplier || !r->shift)
-            throw bad_arg(RS + ": null multiplier or shift");
-        if (r->channels != 1 && r->channels != oc)
-            throw invalid(RS, "multiplier and shift must have 1 or " + std::to_string(oc) + " elements");
-        const DType out_t = static_cast<DType>(r->output_dtype);
-        if (out_t != DT_INT8 && out_t != DT_INT16 && out_t != DT_INT32)
-            throw Error(ERR_DTYPE_MISMATCH, RS + ": unsupported types INT32 -> " + dtype_name(out_t));
-        if (out_t == DT_INT8 ? (r->output_zp < -128 || r->output_zp > 127) : r->output_zp != 0)
-            throw invalid(RS, "zero point not allowed for this type");
-        RescaleDev& rs = c.rs;
-        rs.channels = r->channels;
-        rs.per_channel = r->channels > 1 ? 1 : 0;
-        rs.scale32 = 1;
-        rs.rounding = r->double_round ? 3 : 1;
-        rs.in_bits = 32;
-        rs.in_unsigned = 0;
-        rs.in_zp = 0;
-        rs.out_zp = r->output_zp;
-        const int bits = out_t == DT_INT8 ? 8 : out_t == DT_INT16 ? 16 : 32;
-        rs.lo = -(int64_t(1) << (bits - 1));
-        rs.hi = (int64_t(1) << (bits - 1)) - 1;
-        rs.out_bytes = bits / 8;
-        if (r->has_clamp) {
-            if (r->clamp_min < rs.lo || r->clamp_max > rs.hi)
-                throw invalid("CLAMP", "min_val and max_val must be values of the output type");
-            if (r->clamp_max < r->clamp_min)
-                throw invalid("CLAMP", "max_val must not be smaller than min_val");
-            rs.has_clamp = 1;
-            rs.clamp_lo = r->clamp_min;
-            rs.clamp_hi = r->clamp_max;
-        }
-        rs.max_shift = 2;
-        rs.min_shift = 62;
-        c.params.resize(size_t(2 * r->channels));
-        for (int32_t i = 0; i < r->channels; i++) {
-            const int32_t m = r->multiplier[i], s = r->shift[i];
-            if (c.count > 0 && (m < 0 || s < 2 || s > 62))
-                throw Error(ERR_GRAPH, "apply_scale_32: invalid multiplier " + std::to_string(m) + " or shift " +
-                                           std::to_string(s));
-            c.params[size_t(i)] = m;
-            c.params[size_t(r->channels + i)] = s;
-            rs.max_shift = std::max(rs.max_shift, s);
-            rs.min_shift = std::min(rs.min_shift, s);
-        }
+    if (a.rescale) {
+        parse_rescale(*a.rescale, oc, c.count, c.rs, c.params);
         c.has_rs = true;
-        c.epi_ok = kern::conv_i8_fast_epilogue_ok(rs);
+        c.epi_ok = kern::conv_i8_fast_epilogue_ok(c.rs);
     }
 
     // Workspace layout: multiplier and shift words, the epilogue table,
@@ -319,6 +329,88 @@ void conv2d_i8_noalloc(const ConvI8Args& a, int64_t* out_shape)
     if (!c.params.empty())
         upload_words(c.params, reinterpret_cast<int32_t*>(ws + c.params_off), s);
     launch_conv2d_i8(c, ws, a.out, err, s);
+}
+
+void matmul_i8(const MatmulI8OpArgs& a, int64_t* out_shape)
+{
+    const std::string MM = "MATMUL";
+    if (!a.a || !a.b || !a.a_shape || !a.b_shape)
+        throw bad_arg(MM + ": null operand or shape pointer");
+    for (int i = 0; i < 3; i++)
+        if (a.a_shape[i] < 1 || a.b_shape[i] < 1)
+            throw Error(ERR_SHAPE_MISMATCH, MM + ": every dimension of a and b must be positive");
+    const int64_t n = a.a_shape[0], h = a.a_shape[1], c = a.a_shape[2], w = a.b_shape[2];
+    // src/ops/matmul.rs:112-123: b is [N, C, W] with a's N and C.
+    if (a.b_shape[0] != n || a.b_shape[1] != c)
+        throw Error(ERR_SHAPE_MISMATCH, MM + ": b shape [" + std::to_string(a.b_shape[0]) + ", " +
+                                            std::to_string(a.b_shape[1]) + ", " + std::to_string(w) +
+                                            "] incompatible with a shape [" + std::to_string(n) + ", " +
+                                            std::to_string(h) + ", " + std::to_string(c) + "]");
+    if (a.a_zp < -128 || a.a_zp > 127 || a.b_zp < -128 || a.b_zp > 127)
+        throw Error(ERR_DTYPE_MISMATCH, MM + ": zero points must be int8 values");
+    const int64_t count = n * h * w;
+    if (n * h * c >= (int64_t(1) << 31) || n * c * w >= (int64_t(1) << 31) || count >= (int64_t(1) << 31))
+        throw bad_arg(MM + ": operands of 2^31 elements or more are not supported");
+    if (out_shape) {
+        out_shape[0] = n;
+        out_shape[1] = h;
+        out_shape[2] = w;
+    }
+    if (c > INT32_MAX || w > INT32_MAX ||
+        !kern::matmul_i8_direct_applies(int32_t(c), int32_t(w), a.a, a.b))
+        throw Error(ERR_UNSUPPORTED_OP, MM + ": the op-level entry takes 16-byte aligned a and b with C a multiple "
+                                             "of 128 and W of 16; other shapes run through a graph");
+    RescaleDev rs;
+    std::vector<int32_t> params;
+    if (a.rescale) {
+        parse_rescale(*a.rescale, w, count, rs, params);
+        if (!kern::conv_i8_fast_epilogue_ok(rs))
+            throw Error(ERR_UNSUPPORTED_OP, MM + ": this RESCALE runs through a graph");
+    }
+    if (!a.out)
+        return;  // a query of the output shape
+    Stream& ts = thread_stream();
+    const hipStream_t s = a.stream ? static_cast<hipStream_t>(a.stream) : ts.s;
+    uint32_t* err = a.device_error;
+    if (!err) {
+        if (s != ts.s)
+            throw bad_arg(MM + ": device_error is required on a stream other than this thread's");
+        err = ts.err;
+    }
+    // Workspace: multiplier and shift words, then the epilogue table (the
+    // bias-free additive constant C za zb and the RESCALE parameters; the
+    // kernel adds the zero-point sums itself).
+    const int64_t params_off = 0, tab_off = round_up(int64_t(params.size()) * 4, 256);
+    const int64_t bytes = tab_off + round_up(kern::conv_i8_table_words(int32_t(w), 1) * 4, 256);
+    auto* ws = static_cast<uint8_t*>(dev_alloc(size_t(bytes), s));
+    if (!params.empty()) {
+        const size_t pb = params.size() * 4;
+        void* hp = pinned_acquire(pb);
+        std::memcpy(hp, params.data(), pb);
+        hip_check(hipMemcpyAsync(ws + params_off, hp, pb, hipMemcpyHostToDevice, s), "upload RESCALE params");
+        pinned_release(hp, s);
+        rs.mult = reinterpret_cast<const int32_t*>(ws + params_off);
+        rs.shift = rs.mult + rs.channels;
+    }
+    ConvI8Desc td;
+    td.x = a.a;
+    td.w = nullptr;
+    td.bias = nullptr;
+    td.bias_len = 1;
+    td.n = 1;
+    td.ih = td.oh = int32_t(h);
+    td.iw = td.ow = 1;
+    td.ic = int32_t(c);
+    td.oc = int32_t(w);
+    td.zp_x = a.a_zp;
+    td.zp_w = a.b_zp;
+    td.batch = 1;
+    kern::conv_i8_table(td, a.rescale ? &rs : nullptr, ws + tab_off, s);
+    const bool done = kern::matmul_i8_direct(a.a, a.b, int32_t(n), int32_t(h), int32_t(c), int32_t(w), a.a_zp, a.b_zp,
+                                             ws + tab_off, a.rescale ? &rs : nullptr, false, a.out, err, s);
+    dev_free(ws, size_t(bytes), s);
+    if (!done)
+        throw Error(ERR_UNSUPPORTED_OP, MM + ": shape not taken by the one-kernel MATMUL");
 }
 
 }  // namespace tosa
