@@ -71,6 +71,7 @@ WORKLOADS = {
     "cfg5_fp16_conv3x3_64x28x28x128": ("float_conv", dict(dtype="FP16"), True, None),
     "cfg5_bf16_conv1x1_64x28x28x128to512": ("float_conv", dict(dtype="BF16", cout=512, k=1), True, None),
     "cfg5_bf16_matmul_16x2048x2048x2048": ("float_matmul", {}, True, 5),
+    "i16_conv_rescale_64x28x28x128": ("conv_i16", {}, True, None),
 }
 
 

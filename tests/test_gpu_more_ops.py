@@ -236,6 +236,15 @@ def test_conv2d_int16_split(geom, rescale16):
     assert same(run(graph, ins)[out].numpy(), oracle_run(graph, ins)[out].vals)
 
 
+def test_conv2d_int16_benchmark_layer():
+    # The benchmark's int16 layer ([N,28,28,128] x [128,3,3,128] into INT48,
+    # per-channel RESCALE to int16) at two images: every output against the
+    # oracle.
+    from tosa_amd import workloads as W
+    graph, ins, info = W.conv_i16(n=2)
+    assert same(run(graph, ins)[info["out"]].numpy(), oracle_run(graph, ins)[info["out"]].vals)
+
+
 @pytest.mark.parametrize("kind,d", [("MATMUL", 2), ("MATMUL_T", 2), ("MATMUL_T", 1)])
 def test_matmul_int16_split(kind, d):
     n, h, c, w = 2, 64, 128, 96

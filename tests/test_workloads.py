@@ -18,6 +18,7 @@ BUILDERS = [
     ("mobilenet_v2", W.mobilenet_v2, {"n": 1}),
     ("float_conv", W.float_conv, {"n": 1, "h": 6, "w": 6, "cin": 16, "cout": 8}),
     ("float_matmul", W.float_matmul, {"batch": 1, "h": 8, "c": 16, "w": 8}),
+    ("conv_i16", W.conv_i16, {"n": 1, "h": 6, "w": 6, "cin": 64, "cout": 16}),
 ]
 
 

@@ -295,6 +295,38 @@ def float_conv(dtype="BF16", n=64, h=28, w=28, cin=128, cout=128, k=3, cfg=5, ou
     return g.build(["y"]), {"x": (x, dtype)}, info
 
 
+def conv_i16(n=64, h=28, w=28, cin=128, cout=128, k=3, cfg=6):
+    """int16 x int8 CONV2D into INT48 (the reference's i16 conv path) with
+    the per-channel RESCALE to int16 an int16 network requantises with
+    (apply_scale_16): the ResNet-scale layer at 16-bit activations."""
+    r = rng(cfg, 0)
+    x = r.integers(-2 ** 15, 2 ** 15, (n, h, w, cin)).astype(np.int16)
+    wt = i8(rng(cfg, 1), (cout, k, k, cin))
+    # Sums of ~1152 products of uniform int16 and int8 values spread to
+    # ~2^25.5; multiplier ~2^14.5 and shifts 27-30 bring them to ~2^12.
+    bias = rng(cfg, 2).integers(-2 ** 24, 2 ** 24, cout)
+    mult = rng(cfg, 3).integers(2 ** 14, 2 ** 15, cout).astype(np.int16)
+    shift = rng(cfg, 4).integers(27, 31, cout).astype(np.int8)
+    pad = [k // 2] * 4
+    g = GraphBuilder()
+    g.input("x", x.shape, "INT16")
+    g.const("w", wt, "INT8")
+    g.const("b", bias, "INT48")
+    g.const("zx", np.array([0]), "INT16")
+    g.const("zw", np.array([0]), "INT8")
+    g.tensor("acc", [n, h, w, cout], "INT48")
+    g.op("CONV2D", ["x", "w", "b", "zx", "zw"], ["acc"], pad=pad, stride=[1, 1], dilation=[1, 1], acc_type="INT48")
+    g.const("m", mult, "INT16")
+    g.const("s", shift, "INT8")
+    g.const("iz", np.array([0]), "INT48")
+    g.const("oz", np.array([0]), "INT16")
+    g.tensor("y", [n, h, w, cout], "INT16")
+    g.op("RESCALE", ["acc", "m", "s", "iz", "oz"], ["y"], scale32=0, rounding_mode="SINGLE_ROUND", per_channel=1)
+    macs = n * h * w * cout * k * k * cin
+    info = {"macs": macs, "ops": 2 * macs, "bytes": x.nbytes + wt.nbytes + n * h * w * cout * 2, "out": "y"}
+    return g.build(["y"]), {"x": (x, "INT16")}, info
+
+
 def float_matmul(dtype="BF16", batch=16, h=2048, c=2048, w=2048, cfg=5):
     a = _normal(rng(cfg, 10), (batch, h, c), dtype)
     b = _normal(rng(cfg, 11), (batch, c, w), dtype)
