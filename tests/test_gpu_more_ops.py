@@ -203,7 +203,7 @@ def test_cast_large(pair):
 @pytest.mark.parametrize("geom", [((2, 14, 14, 64), 64, 3, [1, 1, 1, 1], [1, 1]),
                                   ((2, 16, 17, 64), 48, 3, [0, 1, 1, 1], [2, 2]),
                                   ((3, 9, 10, 48), 32, 1, [0, 0, 0, 0], [1, 1])])
-@pytest.mark.parametrize("rescale16", [False, True])
+@pytest.mark.parametrize("rescale16", [False, True, "clamp"])
 def test_conv2d_int16_split(geom, rescale16):
     xs, oc, k, pad, stride = geom
     r = rng_for("conv_i16", geom)
@@ -231,9 +231,18 @@ def test_conv2d_int16_split(geom, rescale16):
         g.tensor("q", [xs[0], oh, ow, oc], "INT16")
         g.op("RESCALE", ["y", "m", "s", "iz", "oz"], ["q"], scale32=0, rounding_mode="SINGLE_ROUND", per_channel=1)
         out = "q"
+        if rescale16 == "clamp":
+            g.tensor("qc", [xs[0], oh, ow, oc], "INT16")
+            g.op("CLAMP", ["q"], ["qc"], min_val=(-20000).to_bytes(2, "little", signed=True) + bytes(6),
+                 max_val=(15000).to_bytes(2, "little", signed=True) + bytes(6))
+            out = "qc"
     graph = g.build([out])
     ins = {"x": (x, "INT16")}
-    assert same(run(graph, ins)[out].numpy(), oracle_run(graph, ins)[out].vals)
+    got = run(graph, ins)[out].numpy()
+    assert same(got, oracle_run(graph, ins)[out].vals)
+    if rescale16:
+        # the combine and RESCALE as one kernel, and as two
+        assert np.array_equal(got, run(graph, ins, fusion=False)[out].numpy())
 
 
 def test_conv2d_int16_benchmark_layer():

@@ -359,6 +359,11 @@ void split_i16(const int16_t* x, int64_t count, int8_t* hi, int8_t* lo, hipStrea
 // bias (INT48 as int64) per channel i % channels, or one value, or null.
 void combine_i48(const int32_t* const* parts, const int64_t* coef, int nparts, const int64_t* bias, int32_t bias_len,
                  int32_t channels, int64_t count, int64_t* out, hipStream_t stream);
+// combine_i48 followed by the RESCALE `rs` of its result (rs.in_bits 48),
+// written in the RESCALE's output type.
+void combine_i48_rescale(const int32_t* const* parts, const int64_t* coef, int nparts, const int64_t* bias,
+                         int32_t bias_len, int32_t channels, int64_t count, const RescaleDev& rs, void* out,
+                         uint32_t* err, hipStream_t stream);
 
 // Standalone RESCALE over `count` elements of element code `xe`.
 void rescale(const RescaleDev& rs, ElemCode xe, const void* x, int64_t count, void* out, uint32_t* err,

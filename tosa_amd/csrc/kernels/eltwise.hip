@@ -614,6 +614,35 @@ __global__ void combine_i48_kernel(I48Parts p, int64_t count, int64_t* out)
     out[i] = v < lo ? lo : (v > hi ? hi : v);
 }
 
+// The INT48 combine followed by the RESCALE that reads it: each combined,
+// clamped value goes straight into the RESCALE (eval_rescale's per-element
+// steps, rescale_value), with no int64 tensor in between.
+// Elements below 2^31 (host-checked); the channel of element i, i mod
+// channels, by a multiply-high division.
+__global__ void combine_i48_rescale_kernel(I48Parts p, RescaleDev rs, int32_t count, FastDiv div_c, void* out,
+                                           uint32_t* err)
+{
+    uint32_t e = 0;
+    const int64_t lo = -(int64_t(1) << 47), hi = (int64_t(1) << 47) - 1;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+        const int32_t c = int32_t(i) - int32_t(fdiv(uint32_t(i), div_c)) * p.channels;
+        int64_t v = 0;
+        for (int k = 0; k < p.nparts; k++)
+            v += p.coef[k] * int64_t(p.part[k][i]);
+        if (p.bias)
+            v += p.bias[p.bias_len == 1 ? 0 : c];
+        v = v < lo ? lo : (v > hi ? hi : v);
+        const int ch = rs.per_channel ? c : 0;
+        const int64_t r = rescale_value(v, rs.mult[ch], rs.shift[ch], rs, e);
+        switch (rs.out_bytes) {
+        case 1: static_cast<int8_t*>(out)[i] = int8_t(r); break;
+        case 2: static_cast<int16_t*>(out)[i] = int16_t(r); break;
+        default: static_cast<int32_t*>(out)[i] = int32_t(r); break;
+        }
+    }
+    report(err, e);
+}
+
 }  // namespace
 
 // The residual kernel without per-element checks applies when every REQUIRE
@@ -702,6 +731,26 @@ void combine_i48(const int32_t* const* parts, const int64_t* coef, int nparts, c
     p.channels = channels;
     if (count > 0)
         hipLaunchKernelGGL(combine_i48_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, p, count, out);
+}
+
+void combine_i48_rescale(const int32_t* const* parts, const int64_t* coef, int nparts, const int64_t* bias,
+                         int32_t bias_len, int32_t channels, int64_t count, const RescaleDev& rs, void* out,
+                         uint32_t* err, hipStream_t stream)
+{
+    I48Parts p{};
+    p.nparts = nparts;
+    for (int k = 0; k < nparts; k++) {
+        p.part[k] = parts[k];
+        p.coef[k] = coef[k];
+    }
+    p.bias = bias;
+    p.bias_len = bias_len;
+    p.channels = channels;
+    if (count >= (int64_t(1) << 31) || channels < 1 || (rs.per_channel && rs.channels != channels))
+        throw std::runtime_error("combine_i48_rescale: unsupported size or channel count");
+    if (count > 0)
+        hipLaunchKernelGGL(combine_i48_rescale_kernel, dim3(grid_for(count)), dim3(256), 0, stream, p, rs,
+                           int32_t(count), FastDiv(uint32_t(channels)), out, err);
 }
 
 void max_pool2d(const PoolDesc& d, bool ignore, float lowest, const void* x, void* out, hipStream_t stream)

@@ -490,7 +490,7 @@ struct FusedTail {
     RescalePrep rp;
 };
 
-std::optional<FusedTail> plan_tail(const ExecState& st, size_t head, const Shape& shape)
+std::optional<FusedTail> plan_tail(const ExecState& st, size_t head, const Shape& shape, DType head_t = DT_INT32)
 {
     if (!st.opts.fusion || !st.plan)
         return std::nullopt;
@@ -508,7 +508,7 @@ std::optional<FusedTail> plan_tail(const ExecState& st, size_t head, const Shape
     tmp.name = rop.inputs[0];
     tmp.shape = shape;
     tmp.data = std::make_shared<Storage>();
-    tmp.data->dtype = DT_INT32;
+    tmp.data->dtype = head_t;
     tmp.data->count = shape_count(shape);
     FusedTail f;
     f.rop = &rop;
@@ -544,18 +544,19 @@ std::optional<FusedTail> plan_tail(const ExecState& st, size_t head, const Shape
 // a CLAMP follows) the RESCALE result become virtual tensors recomputed on
 // demand; the last output is the one the fused kernel wrote.
 void finish_fused(ExecState& st, const std::string& head_out, const Shape& shape, const FusedTail& f,
-                  const TensorPtr& final_out, std::function<void(Storage&)> head_fill)
+                  const TensorPtr& final_out, std::function<void(Storage&)> head_fill, DType head_t = DT_INT32)
 {
-    auto head = virtual_output(head_out, shape, DT_INT32, std::move(head_fill));
+    auto head = virtual_output(head_out, shape, head_t, std::move(head_fill));
     st.set(head);
     if (f.cop) {
         RescalePrep rp = f.rp;
         rp.rs.has_clamp = 0;
         auto src = head;
-        auto mid = virtual_output(f.rop->outputs[0], shape, rp.out_t, [src, rp](Storage& out) {
+        const ElemCode he = elem_code(head_t);
+        auto mid = virtual_output(f.rop->outputs[0], shape, rp.out_t, [src, rp, he](Storage& out) {
             Stream& s = thread_stream();
             const void* x = src->data->device_in();
-            kern::rescale(rp.rs, E_I32, x, out.count, out.device_out(), s.err, s.s);
+            kern::rescale(rp.rs, he, x, out.count, out.device_out(), s.err, s.s);
         });
         st.pending[f.rop->outputs[0]] = mid;
         st.pending[f.cop->outputs[0]] = make_tensor(f.cop->outputs[0], shape, final_out->data);
@@ -1220,12 +1221,36 @@ void eval_conv(ExecState& st, const Operator& op, size_t index, bool depthwise)
             auto pl = make_device_storage(DT_INT32, count);
             conv_i8_fast(fd, th->device_in(), nullptr, ph->device_out(), st.err(), s);
             conv_i8_fast(dl, tl->device_in(), nullptr, pl->device_out(), st.err(), s);
-            auto out = new_output(out_name, g.out_shape, DT_INT48);
             const int32_t* parts[2] = {static_cast<const int32_t*>(ph->device_in()),
                                        static_cast<const int32_t*>(pl->device_in())};
             const int64_t coef[2] = {256, 1};
-            kern::combine_i48(parts, coef, 2, static_cast<const int64_t*>(bias->data->device_in()), int32_t(bc),
-                              int32_t(g.oc), count, static_cast<int64_t*>(out->data->device_out()), s);
+            const int64_t* bdev = static_cast<const int64_t*>(bias->data->device_in());
+            const int32_t oc = int32_t(g.oc);
+            if (auto tail = plan_tail(st, index, g.out_shape, DT_INT48)) {
+                // The RESCALE (and CLAMP) after the convolution read the
+                // combined values directly; the INT48 tensor is made only if
+                // something asks for it.
+                auto fin = new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], g.out_shape,
+                                      tail->rp.out_t);
+                kern::combine_i48_rescale(parts, coef, 2, bdev, int32_t(bc), oc, count, tail->rp.rs,
+                                          fin->data->device_out(), st.err(), s);
+                auto keep = tail->rp.params;
+                finish_fused(
+                    st, out_name, g.out_shape, *tail, fin,
+                    [ph, pl, bias, bc, oc, count, keep](Storage& o) {
+                        Stream& ts = thread_stream();
+                        const int32_t* p2[2] = {static_cast<const int32_t*>(ph->device_in()),
+                                                static_cast<const int32_t*>(pl->device_in())};
+                        const int64_t c2[2] = {256, 1};
+                        kern::combine_i48(p2, c2, 2, static_cast<const int64_t*>(bias->data->device_in()),
+                                          int32_t(bc), oc, count, static_cast<int64_t*>(o.device_out()), ts.s);
+                    },
+                    DT_INT48);
+                return;
+            }
+            auto out = new_output(out_name, g.out_shape, DT_INT48);
+            kern::combine_i48(parts, coef, 2, bdev, int32_t(bc), oc, count,
+                              static_cast<int64_t*>(out->data->device_out()), s);
             st.set(out);
             return;
         }
