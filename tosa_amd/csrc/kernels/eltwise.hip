@@ -587,6 +587,27 @@ __global__ void split_i16_kernel(const int16_t* x, int64_t count, int8_t* hi, in
     lo[i] = int8_t((v & 255) - 128);
 }
 
+// The same, 8 values per thread (16-byte loads, 8-byte stores) for 16-byte
+// aligned x, 8-byte aligned halves and a count that is a multiple of 8.
+__global__ void split_i16_x8_kernel(const uint4* x, int64_t count8, uint2* hi, uint2* lo)
+{
+    for (int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; q < count8; q += int64_t(gridDim.x) * blockDim.x) {
+        const uint4 v = x[q];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t h[2], l[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            // high bytes of the four int16 values in words 2k, 2k + 1 (v_perm_b32:
+            // selector bytes 0-3 pick the second operand, 4-7 the first); low
+            // bytes likewise, then each offset by -128 (bit 7 flipped).
+            h[k] = __builtin_amdgcn_perm(w[2 * k + 1], w[2 * k], 0x07050301u);
+            l[k] = __builtin_amdgcn_perm(w[2 * k + 1], w[2 * k], 0x06040200u) ^ 0x80808080u;
+        }
+        hi[q] = uint2{h[0], h[1]};
+        lo[q] = uint2{l[0], l[1]};
+    }
+}
+
 // INT48 result of products of int16 operands assembled from int32 partial
 // sums of their int8 halves: out = clamp48(sum_k coef[k] part[k] + bias),
 // in int64 (the reference's AccI64 and its final clamp, src/ops/conv.rs:
@@ -713,7 +734,15 @@ void avg_pool2d(const PoolDesc& d, const void* x, void* out, uint32_t* err, hipS
 
 void split_i16(const int16_t* x, int64_t count, int8_t* hi, int8_t* lo, hipStream_t stream)
 {
-    if (count > 0)
+    if (count <= 0)
+        return;
+    const bool x8 = count % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                    (reinterpret_cast<uintptr_t>(hi) | reinterpret_cast<uintptr_t>(lo)) % 8 == 0;
+    if (x8)
+        hipLaunchKernelGGL(split_i16_x8_kernel, dim3(grid_for(count / 8)), dim3(256), 0, stream,
+                           reinterpret_cast<const uint4*>(x), count / 8, reinterpret_cast<uint2*>(hi),
+                           reinterpret_cast<uint2*>(lo));
+    else
         hipLaunchKernelGGL(split_i16_kernel, dim3(blocks_for(count, 256)), dim3(256), 0, stream, x, count, hi, lo);
 }
 
