@@ -273,3 +273,34 @@ def test_matmul_int16_split(kind, d):
     graph = g.build(["y"])
     ins = {"a": (a, "INT16"), "b": (b, "INT16")}
     assert same(run(graph, ins)["y"].numpy(), oracle_run(graph, ins)["y"].vals)
+
+
+def test_matmul_int16_rescale_fused():
+    # INT48 MATMUL followed by a per-column RESCALE to int16 (apply_scale_16)
+    # and a CLAMP: the combine and the RESCALE run as one kernel; the result
+    # must match the oracle and the unfused run.
+    n, h, c, w = 2, 40, 128, 48
+    r = rng_for("mm_i16_rescale")
+    a = r.integers(-2 ** 15, 2 ** 15, (n, h, c)).astype(np.int16)
+    b = r.integers(-2 ** 15, 2 ** 15, (n, c, w)).astype(np.int16)
+    g = GraphBuilder()
+    g.input("a", [n, h, c], "INT16")
+    g.input("b", [n, c, w], "INT16")
+    g.const("az", np.array([0]), "INT16")
+    g.const("bz", np.array([0]), "INT16")
+    g.tensor("y", [n, h, w], "INT48")
+    g.op("MATMUL", ["a", "b", "az", "bz"], ["y"])
+    g.const("m", r.integers(2 ** 14, 2 ** 15, w).astype(np.int16), "INT16")
+    g.const("s", r.integers(30, 36, w).astype(np.int8), "INT8")
+    g.const("iz", np.array([0]), "INT48")
+    g.const("oz", np.array([0]), "INT16")
+    g.tensor("q", [n, h, w], "INT16")
+    g.op("RESCALE", ["y", "m", "s", "iz", "oz"], ["q"], scale32=0, rounding_mode="SINGLE_ROUND", per_channel=1)
+    g.tensor("qc", [n, h, w], "INT16")
+    g.op("CLAMP", ["q"], ["qc"], min_val=(-20000).to_bytes(2, "little", signed=True) + bytes(6),
+         max_val=(15000).to_bytes(2, "little", signed=True) + bytes(6))
+    graph = g.build(["qc"])
+    ins = {"a": (a, "INT16"), "b": (b, "INT16")}
+    got = run(graph, ins)["qc"].numpy()
+    assert same(got, oracle_run(graph, ins)["qc"].vals)
+    assert np.array_equal(got, run(graph, ins, fusion=False)["qc"].numpy())

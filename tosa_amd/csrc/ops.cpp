@@ -1566,11 +1566,34 @@ void eval_matmul(ExecState& st, const Operator& op, size_t index, bool transpose
         };
         const StoragePtr p[4] = {part(ah, bhr, 0, 0), part(ah, blr, 0, -128), part(al, bhr, -128, 0),
                                  part(al, blr, -128, -128)};
-        auto out = new_output(out_name, out_shape, DT_INT48);
         const int32_t* parts[4];
         for (int k = 0; k < 4; k++)
             parts[k] = static_cast<const int32_t*>(p[k]->device_in());
         const int64_t coef[4] = {65536, 256, 256, 1};
+        if (auto tail = plan_tail(st, index, out_shape, DT_INT48)) {
+            // The RESCALE (and CLAMP) after the MATMUL read the combined
+            // values directly (channels: the columns w).
+            auto fin = new_output(tail->cop ? tail->cop->outputs[0] : tail->rop->outputs[0], out_shape,
+                                  tail->rp.out_t);
+            kern::combine_i48_rescale(parts, coef, 4, nullptr, 1, int32_t(w), count, tail->rp.rs,
+                                      fin->data->device_out(), st.err(), s);
+            auto keep = tail->rp.params;
+            const StoragePtr q0 = p[0], q1 = p[1], q2 = p[2], q3 = p[3];
+            finish_fused(
+                st, out_name, out_shape, *tail, fin,
+                [q0, q1, q2, q3, count, keep](Storage& o) {
+                    Stream& ts = thread_stream();
+                    const int32_t* p4[4] = {static_cast<const int32_t*>(q0->device_in()),
+                                            static_cast<const int32_t*>(q1->device_in()),
+                                            static_cast<const int32_t*>(q2->device_in()),
+                                            static_cast<const int32_t*>(q3->device_in())};
+                    const int64_t c4[4] = {65536, 256, 256, 1};
+                    kern::combine_i48(p4, c4, 4, nullptr, 1, 1, count, static_cast<int64_t*>(o.device_out()), ts.s);
+                },
+                DT_INT48);
+            return;
+        }
+        auto out = new_output(out_name, out_shape, DT_INT48);
         kern::combine_i48(parts, coef, 4, nullptr, 1, 1, count, static_cast<int64_t*>(out->data->device_out()), s);
         st.set(out);
         return;
